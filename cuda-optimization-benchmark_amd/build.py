@@ -1,0 +1,109 @@
+"""Build libtaskops.so (all kernels + the C ABI of include/taskops.h) and the per-op
+drop-in libraries for gfx950 with hipcc, in-tree under `lib/`.
+
+    __graft_entry__.build()   (the package directory name is not an importable identifier;
+                               __graft_entry__.load_package() imports it as `cob_amd`)
+
+The drop-in libraries (`lib/dropin_<op>.so`) each hold the C++ `void reference(...)`
+overload of one task plus the grader's `extern "C" void grader_entry(void**)` shim,
+linked against libtaskops.so, so the reference benchmark's ctypes driver
+(graders/child.py:79-100) can load one per task unchanged.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "lib"
+OBJ = PKG / "_build"
+INCLUDE = ROOT / "include"
+
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Packed-fp32 VALU forms are disabled for all device code (they have given silently
+# wrong results on this pool); hipcc's host pass warns that it does not know the feature.
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-munsafe-fp-atomics", "-Wno-unused-command-line-argument",
+    f"-I{INCLUDE}", f"-I{CSRC}",
+]
+
+# Per-file extra flags.  leaky must not contract beta*mem + x into an FMA: the spec
+# rounds every operation (the source also sets `#pragma clang fp contract(off)`).
+EXTRA = {
+    "leaky.hip": ["-ffp-contract=off"],
+}
+
+KERNEL_SOURCES = [
+    "runtime.hip",
+    "pow_abs_sqrt_mean.hip",
+    "ppo_clip.hip",
+    "reward_to_go.hip",
+    "leaky.hip",
+    "efficient_kan.hip",
+    "fp8_linear.hip",
+]
+
+OPS = ["pow_abs_sqrt_mean", "leaky", "reward_to_go", "ppo_clip", "efficient_kan", "fp8_linear"]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    r = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+
+
+def _compile(src: str) -> Path:
+    out = OBJ / (Path(src).stem + ".o")
+    cmd = [HIPCC, *COMMON, *EXTRA.get(src, []), "-c", str(CSRC / src), "-o", str(out)]
+    _run(cmd)
+    return out
+
+
+def dropin_source(op: str) -> str:
+    """The grader shim for one op, generated from the task's signature the way
+    graders/grade.py:85-89 generates it, with dropin.hpp standing in for solution.cu."""
+    from .grader.shim import parse_signature, shim_source
+    from .tasks import load_task
+    return shim_source(parse_signature(load_task(op)["hip_signature"]))
+
+
+def build(verbose: bool = True, jobs: int | None = None) -> Path:
+    """Compile every HIP source for gfx950 and link lib/libtaskops.so plus the drop-ins."""
+    if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
+        raise RuntimeError(f"hipcc not found at {HIPCC}")
+    OBJ.mkdir(parents=True, exist_ok=True)
+    LIB.mkdir(parents=True, exist_ok=True)
+    jobs = jobs or min(8, os.cpu_count() or 4)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, KERNEL_SOURCES))
+    lib = LIB / "libtaskops.so"
+    tmp = LIB / "libtaskops.so.tmp"
+    _run([HIPCC, *COMMON, "-shared", "-o", str(tmp), *map(str, objs), "-Wl,-Bsymbolic"])
+    os.replace(tmp, lib)
+
+    def _dropin(op: str) -> Path:
+        src = OBJ / f"dropin_{op}.hip"
+        src.write_text(dropin_source(op))
+        out = LIB / f"dropin_{op}.so"
+        t = LIB / f"dropin_{op}.so.tmp"
+        _run([HIPCC, *COMMON, "-shared", "-o", str(t), str(src), f"-L{LIB}", "-ltaskops",
+              "-Wl,-rpath,$ORIGIN", "-Wl,-Bsymbolic"])
+        os.replace(t, out)
+        return out
+
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        list(ex.map(_dropin, OPS))
+    if verbose:
+        print(f"built {lib} and {len(OPS)} drop-in libraries", flush=True)
+    return lib
+
+

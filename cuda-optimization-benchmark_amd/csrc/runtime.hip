@@ -1,0 +1,64 @@
+// Host runtime of libtaskops: per-device cached workspaces and device facts.
+#include <mutex>
+#include <vector>
+
+#include "common.hpp"
+
+namespace taskops {
+namespace {
+
+constexpr int kMaxDevices = 64;
+
+struct Region {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+std::mutex g_mu;
+Region g_regions[kMaxDevices][kNumSlots];
+// Buffers replaced by a larger one stay allocated until exit: a kernel enqueued before
+// the replacement may still be using them, and freeing would need a host sync.
+std::vector<void*> g_retired;
+int g_cus[kMaxDevices] = {0};
+
+}  // namespace
+
+hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_mu);
+  Region& r = g_regions[dev][slot];
+  if (r.bytes < bytes) {
+    size_t want = bytes < 4096 ? 4096 : bytes;
+    void* p = nullptr;
+    e = hipMalloc(&p, want);
+    if (e != hipSuccess) return e;
+    e = hipMemsetAsync(p, 0, want, stream);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return e;
+    }
+    if (r.ptr) g_retired.push_back(r.ptr);
+    r.ptr = p;
+    r.bytes = want;
+  }
+  *out = r.ptr;
+  return hipSuccess;
+}
+
+int device_cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  int n = __atomic_load_n(&g_cus[dev], __ATOMIC_RELAXED);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+    n = 256;
+  __atomic_store_n(&g_cus[dev], n, __ATOMIC_RELAXED);
+  return n;
+}
+
+}  // namespace taskops
+
+extern "C" int taskops_version(void) { return 1; }

@@ -1,0 +1,112 @@
+/*
+ * taskops.h — C ABI of the MI355X (gfx950) task-op library `libtaskops.so`.
+ *
+ * Each entry point replaces one task op of Mohamed-Alaboudi/cuda-optimization-benchmark,
+ * whose public interface is a C++ `void reference(...)` per task (the signature in
+ * tasks/<id>/tests/task.json:3, implemented by reference/<id>/solution.cu).  The
+ * arguments keep that signature's order, meaning and scalar types; two things are added:
+ *
+ *   - the HIP stream the work is enqueued on (NULL = the default stream, as the
+ *     reference's prompts require: "Launch your work on the default stream");
+ *   - a return value: hipSuccess (0) or the hipError_t of the failed launch or argument
+ *     check.  The reference's `void` entry has no error channel (errors surface at the
+ *     caller's next synchronize); the C++ drop-in overloads in dropin.hip keep `void`.
+ *
+ * All pointers are device pointers to contiguous row-major data, owned by the caller.
+ * The library keeps one small cached workspace per device (allocated on the first call
+ * that needs it, never freed before exit) and never caches results or derived weight
+ * contents between calls.  Calls are asynchronous: no host synchronisation and no
+ * device-to-host copy happens inside a call.  Calls that share a device and overlap in
+ * time on different streams race on that workspace (as the reference's statics do);
+ * calls on one stream are safe.
+ *
+ * Raw-bit types are used at the boundary for the two non-C element types:
+ *   e4m3 (OCP FP8, 1 byte)  -> uint8_t   (the reference uses __nv_fp8_e4m3)
+ *   bfloat16 (2 bytes)      -> uint16_t  (the reference uses __nv_bfloat16)
+ */
+#ifndef TASKOPS_H_
+#define TASKOPS_H_
+
+#include <hip/hip_runtime_api.h>
+#include <stdbool.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Library version; bumps when an entry point's behaviour changes. */
+int taskops_version(void);
+
+/* output[0] = mean over n = batch_size*4*height*width elements of
+ * sqrt((inp - target)^2 + 1e-6), fp32 result of an fp64 reduction.  n == 0 writes NaN
+ * (the mean of nothing, as reference_exact gives); a negative dimension returns
+ * hipErrorInvalidValue and writes nothing.
+ * Replaces: reference/pow_abs_sqrt_mean/solution.cu:99-118
+ *           (tasks/pow_abs_sqrt_mean/tests/task.json:3; op: reference.py:22-28). */
+hipError_t taskops_pow_abs_sqrt_mean(const float* inp, const float* target,
+                                     int64_t batch_size, int64_t height, int64_t width,
+                                     float* output, hipStream_t stream);
+
+/* Leaky integrate-and-fire layer, reset by subtraction, T steps over B*H neurons.
+ * beta is clamped to [0,1]; per step: reset = (mem >= th); mem = beta*mem + x[t] - reset*th
+ * (each operation rounded in fp32, no contraction); spikes[t] = (mem >= th).
+ * Bit-identical to the fp32 step-by-step reference.
+ * Replaces: reference/leaky/solution.cu:106-138 (tasks/leaky/tests/task.json:3;
+ *           op: tasks/leaky/reference.py:26-37). */
+hipError_t taskops_leaky(const float* input_current, const float* mem0, const float* beta,
+                         const float* threshold, int32_t T, int32_t B, int32_t H,
+                         float* spikes, float* final_mem, hipStream_t stream);
+
+/* output[b,t] = reward[b,t] + gamma * (done[b,t] ? 0 : output[b,t+1]), output[b,T] = 0.
+ * Affine scan carried in fp64, one rounding to fp32 per element.  B <= 0 or T <= 0 does
+ * nothing.
+ * Replaces: reference/reward_to_go/solution.cu:237-264
+ *           (tasks/reward_to_go/tests/task.json:3; op: reference.py:34-42). */
+hipError_t taskops_reward_to_go(const float* reward, const bool* done, float gamma,
+                                int32_t B, int32_t T, float* output, hipStream_t stream);
+
+/* PPO clipped objective and metrics over N = B*T*H samples, one pass, one launch.
+ * output[0..5] = [loss_objective, clip_fraction, approx_kl, ess, max_ratio, mean_ratio].
+ * Replaces: reference/ppo_clip/solution.cu:165-182 (tasks/ppo_clip/tests/task.json:3;
+ *           op: tasks/ppo_clip/reference.py:27-39). */
+hipError_t taskops_ppo_clip(int32_t B, int32_t T, int32_t H, const float* current_log_prob,
+                            const float* old_log_prob, const float* advantage,
+                            float clip_epsilon, float* output, hipStream_t stream);
+
+/* The same single pass, also reading a per-sample entropy:
+ * output[0..7] = [loss_objective, clip_fraction, approx_kl, ess, max_ratio, mean_ratio,
+ *                 mean_entropy, loss_entropy = -entropy_coef * mean_entropy].
+ * Has no counterpart in the reference; it is the ClipPPOLoss entropy bonus term that the
+ * benchmark's BASELINE configuration adds (TorchRL ClipPPOLoss, entropy_coef). */
+hipError_t taskops_ppo_clip_entropy(int32_t B, int32_t T, int32_t H,
+                                    const float* current_log_prob, const float* old_log_prob,
+                                    const float* advantage, const float* entropy,
+                                    float clip_epsilon, float entropy_coef, float* output,
+                                    hipStream_t stream);
+
+/* KANLinear forward: out[B,O] = silu(x) @ base_weight^T
+ *                              + bsplines(x; grid) @ (spline_weight * spline_scaler[...,None])^T
+ * grid is [I, grid_size + 2*spline_order + 1] (per-feature knots, strictly increasing),
+ * spline_weight is [O, I, grid_size + spline_order].  fp32 in and out.
+ * Replaces: reference/efficient_kan/solution.cu:177-288
+ *           (tasks/efficient_kan/tests/task.json:3; op: reference.py:33-51). */
+hipError_t taskops_efficient_kan(const float* x, const float* grid, const float* base_weight,
+                                 const float* spline_weight, const float* spline_scaler,
+                                 int32_t grid_size, int32_t spline_order, int32_t B, int32_t I,
+                                 int32_t O, float* out, hipStream_t stream);
+
+/* FP8 (OCP e4m3) linear: output[M,N] = bf16( (x/scale_x) @ (w/scale_w)^T + bias ),
+ * x [M,K] and w [N,K] row-major e4m3 bytes, bias [N] bf16, fp32 accumulation, one
+ * round-to-nearest-even to bf16.
+ * Replaces: reference/fp8_linear/solution.cu:276-321 (tasks/fp8_linear/tests/task.json:3;
+ *           op: tasks/fp8_linear/reference.py:34-41). */
+hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_fp8,
+                              float scale_x, const uint8_t* w_fp8, float scale_w,
+                              const uint16_t* bias, uint16_t* output, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TASKOPS_H_ */

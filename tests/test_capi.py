@@ -1,0 +1,46 @@
+"""The C ABI on the CPU: libtaskops.so loads and exports every symbol include/taskops.h
+declares; each drop-in library exports `grader_entry` and its C++ `reference` overload.
+No compute call is made (no GPU here)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from cob_amd import LIB_DIR, capi, tasks
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "taskops.h"
+
+
+def declared_symbols():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(taskops_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_binding_table():
+    assert declared_symbols() == sorted(capi.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = capi.load()
+    assert lib.taskops_version() >= 1
+    for sym in declared_symbols():
+        assert hasattr(lib, sym), sym
+    dyn = subprocess.run(["nm", "-D", "--defined-only", str(capi.lib_path())], capture_output=True, text=True).stdout
+    for sym in declared_symbols():
+        assert re.search(rf"\bT {sym}$", dyn, re.M), sym
+
+
+@pytest.mark.parametrize("op", tasks.OPS)
+def test_dropin_exports(op):
+    p = LIB_DIR / f"dropin_{op}.so"
+    lib = ctypes.CDLL(str(p))
+    assert hasattr(lib, "grader_entry")
+    dyn = subprocess.run(["nm", "-D", "-C", "--defined-only", str(p)], capture_output=True, text=True).stdout
+    assert re.search(r"\breference\(", dyn), dyn
+
+
+def test_missing_library_fails_loudly(tmp_path):
+    with pytest.raises(capi.TaskOpsError):
+        capi.load(tmp_path / "libtaskops.so")
