@@ -46,24 +46,42 @@ __device__ __forceinline__ double block_sum(double v, double* lds) {
 }
 
 // ---------------------------------------------------------------------------------------
-// Single-launch grid reduction support.
+// Single-launch grid reduction: publish a per-workgroup record, take a ticket, and let
+// the last workgroup to arrive combine the records in a fixed order.
 //
-// Every workgroup writes its partial record, then thread 0 takes a ticket with an
-// agent-scope acq_rel atomic.  MI355X has 8 XCDs with private L2s: the release half
-// writes the partial back past this XCD's L2 and the acquire half, taken by the last
-// workgroup, invalidates stale lines before it reads the other XCDs' partials.  The
-// last workgroup resets the ticket, so the next launch starts from zero.
+// MI355X has 8 XCDs with private L2s.  An agent-scope release (fence or acq_rel atomic)
+// writes this XCD's whole L2 back; done by every workgroup it serialises per XCD and
+// costs ~0.1 us per workgroup (measured: +190 us at 2048 workgroups).  Atomic RMWs at
+// agent scope are instead performed at the device coherence point, so each workgroup
+// publishes its record with agent-scope atomic exchanges, waits until they have
+// returned, and only then increments the ticket (a relaxed agent-scope RMW).  The ticket
+// value 0..G-1 therefore orders every exchange before the last arrival's ticket RMW, and
+// the last workgroup reads the records with agent-scope atomic loads, which read the
+// coherence point.  The last workgroup resets the ticket for the next launch.
 // ---------------------------------------------------------------------------------------
-__device__ __forceinline__ bool arrive_is_last(unsigned* ticket, bool* lds_flag) {
-  __syncthreads();  // the whole workgroup's partial stores precede the ticket
+
+// Thread 0 publishes rec[0..n) into slot[0..n) and takes a ticket; every thread of the
+// workgroup learns whether it is the last to arrive.
+template <int kN>
+__device__ __forceinline__ bool publish_and_arrive(double* slot, const double* rec,
+                                                   unsigned* ticket, bool* lds_flag) {
   if (threadIdx.x == 0) {
-    __threadfence();
-    unsigned prev = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned long long seen = 0;
+#pragma unroll
+    for (int f = 0; f < kN; ++f) {
+      seen |= __hip_atomic_exchange(reinterpret_cast<unsigned long long*>(slot) + f,
+                                    __double_as_longlong(rec[f]), __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Consume the exchanges' results so the ticket RMW issues only after they returned.
+    asm volatile("" ::"v"(seen));
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    const unsigned prev = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     *lds_flag = (prev == gridDim.x - 1);
   }
   __syncthreads();
-  bool last = *lds_flag;
-  if (last) __threadfence();  // acquire for every thread of the finishing workgroup
+  const bool last = *lds_flag;
+  if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   return last;
 }
 

@@ -1,0 +1,445 @@
+// fp8_linear kernels for gfx950 (instantiated by fp8_linear.hip):
+// output = bf16((x/sx) @ (w/sw)^T + bias), OCP e4m3 inputs.
+//
+// Op: tasks/fp8_linear/reference.py:34-41 (fp64 oracle :44-45, one rounding to bf16);
+// drop-in signature tasks/fp8_linear/tests/task.json:3, replacing
+// reference/fp8_linear/solution.cu:276-321 (there: dequantise + cuBLASLt).
+//
+// Both operands are K-contiguous e4m3 ([M,K] and [N,K]), which is exactly the operand
+// layout of gfx950's scaled MFMA v_mfma_scale_f32_16x16x128_f8f6f4 (format 0 = e4m3,
+// block scales set to 2^0): lane l supplies 32 consecutive k of row (l % 16) starting at
+// k = 32*(l / 16), for A and B alike, and gets back D rows 4*(l/16)..+3 of column l % 16.
+// The product is accumulated in fp32 and the epilogue applies 1/(sx*sw), adds the bf16
+// bias and rounds to bf16 (nearest-even) once.
+//
+// Two kernels, one launch per call:
+//  * tiled (M > 64): 256x256 output tile per workgroup of 4 waves (one per SIMD, each
+//    128x128 = 8x8 MFMA blocks whose 256 fp32 accumulators sit in AGPRs), K in steps of
+//    128 staged through LDS (2 stages x 64 KiB, 16-byte
+//    chunks XOR-swizzled by row so a wave's fragment reads spread over the banks).  The
+//    next K-step's global loads are in flight while the current one feeds the MFMAs.
+//    Workgroups are mapped so that each XCD's 32 concurrent tiles form a 4x8 block of
+//    the output and share A/B panels in that XCD's L2.
+//  * skinny (M <= 64): the weight-streaming case.  A workgroup owns 16 output columns
+//    and all M rows; its 8 waves split K, read W straight from global memory into MFMA
+//    fragments, and reduce their partial tiles through LDS in a fixed order.
+#pragma once
+
+#include "common.hpp"
+
+namespace taskops {
+namespace fp8 {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kScaleOne = 0x7f7f7f7f;  // E8M0 127 in every byte: 2^0
+
+__device__ __forceinline__ f32x4 mfma_e4m3(i32x8 a, i32x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, kScaleOne, 0, kScaleOne);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  unsigned u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
+
+// Buffer resources: a 128-bit descriptor (base, byte size) makes the hardware return zero
+// for loads past the size and drop stores past it, so tile tails need no branches.
+// Offsets are 32-bit, so each workgroup bases its descriptors at its own tile.
+constexpr int kRawBufferFlags = 0x00020000;  // raw (untyped) 32-bit buffer, gfx9 layout
+constexpr unsigned kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, size_t bytes) {
+  const int n = bytes > 0x7fffffffu ? 0x7fffffff : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, kRawBufferFlags);
+}
+
+// 16 bytes of a K-contiguous row starting at column k, zero past K.  `off` is the byte
+// offset of (row, k) in the descriptor, or kOutOfRange for rows past the matrix.
+// kVec 16: K % 16 == 0, a chunk is wholly inside or outside K; 8: K % 8 == 0, two
+// independent halves; 1: any K, byte by byte.
+template <int kVec>
+__device__ __forceinline__ i32x4 load16(__amdgpu_buffer_rsrc_t r, unsigned off, int k, int K) {
+  if constexpr (kVec == 16) {
+    const unsigned o = k < K ? off : kOutOfRange;
+    return __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(r, o, 0, 0));
+  } else if constexpr (kVec == 8) {
+    const unsigned o0 = k < K ? off : kOutOfRange;
+    const unsigned o1 = k + 8 < K ? off + 8 : kOutOfRange;
+    const i32x2 lo = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o0, 0, 0));
+    const i32x2 hi = __builtin_bit_cast(i32x2, __builtin_amdgcn_raw_buffer_load_b64(r, o1, 0, 0));
+    return i32x4{lo.x, lo.y, hi.x, hi.y};
+  } else {
+    unsigned w[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const unsigned o = (k + i < K && off != kOutOfRange) ? off + i : kOutOfRange;
+      w[i / 4] |= (unsigned)__builtin_amdgcn_raw_buffer_load_b8(r, o, 0, 0) << (8 * (i % 4));
+    }
+    return i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+  }
+}
+
+__device__ __forceinline__ i32x8 join(i32x4 a, i32x4 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// ---------------------------------------------------------------------------------------
+// Tiled kernel
+// ---------------------------------------------------------------------------------------
+constexpr int BM = 256, BN = 256, BK = 128;
+constexpr int kThreads = 256;
+constexpr int kWavesN = 2;                       // waves arranged 2 (M) x 2 (N)
+constexpr int WM = 128, WN = 128;                // wave tile
+constexpr int kMI = WM / 16, kNJ = WN / 16;      // 16x16 MFMA blocks per wave tile
+constexpr int kStageBytes = (BM + BN) * BK;  // 64 KiB: A tile then B tile
+constexpr int kChunksPerRow = BK / 16;       // 8
+constexpr int kLoadsPerThread = BM * kChunksPerRow / kThreads;  // 16-byte chunks per operand
+
+__device__ __forceinline__ int swizzle(int row, int chunk) {
+  return row * BK + ((chunk ^ (row & 7)) << 4);
+}
+
+// Output tile of workgroup `b` (a bijection onto the tm x tn tiles for any tile counts).
+// Workgroups are dispatched to the 8 XCDs round-robin (b % 8), so when the tile count is
+// a multiple of 8, XCD x is given the contiguous run of virtual tiles
+// [x*T/8, (x+1)*T/8); virtual tiles are then laid out in groups of kGroupM tile rows,
+// column by column, so a run of 32 forms a 4x8 block whose A and B panels stay in that
+// XCD's L2.
+constexpr int kGroupM = 4;
+__device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt) {
+  const int T = tm * tn;
+  const int v = (T % 8 == 0) ? (b % 8) * (T / 8) + b / 8 : b;
+  const int per_group = kGroupM * tn;
+  const int first_m = (v / per_group) * kGroupM;
+  const int rows = min(tm - first_m, kGroupM);
+  const int r = v % per_group;
+  mt = first_m + r % rows;
+  nt = r / rows;
+}
+
+template <int kVec>
+__global__ __launch_bounds__(kThreads) void fp8_gemm_tiled(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
+    float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  int mt, nt;
+  tile_of(blockIdx.x, tm, tn, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;  // wave tile origin (wm*WM, wn*WN)
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t xa = make_rsrc(x + (size_t)m0 * K, (size_t)rows_a * K);
+  const __amdgpu_buffer_rsrc_t wb = make_rsrc(w + (size_t)n0 * K, (size_t)rows_b * K);
+
+  i32x4 ra[kLoadsPerThread], rb[kLoadsPerThread];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      const int row = q / kChunksPerRow, chunk = q % kChunksPerRow;
+      const int gk = k0 + chunk * 16;
+      const unsigned off = (unsigned)(row * K + gk);
+      ra[i] = load16<kVec>(xa, row < rows_a ? off : kOutOfRange, gk, K);
+      rb[i] = load16<kVec>(wb, row < rows_b ? off : kOutOfRange, gk, K);
+    }
+  };
+  auto swrite = [&](int stage) {
+    uint8_t* As = smem + stage * kStageBytes;
+    uint8_t* Bs = As + BM * BK;
+#pragma unroll
+    for (int i = 0; i < kLoadsPerThread; ++i) {
+      const int q = tid + kThreads * i;
+      const int row = q / kChunksPerRow, chunk = q % kChunksPerRow;
+      *reinterpret_cast<i32x4*>(As + swizzle(row, chunk)) = ra[i];
+      *reinterpret_cast<i32x4*>(Bs + swizzle(row, chunk)) = rb[i];
+    }
+  };
+
+  f32x4 acc[kMI][kNJ];
+#pragma unroll
+  for (int i = 0; i < kMI; ++i)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (K + BK - 1) / BK;
+  gload(0);
+  swrite(0);
+  __syncthreads();
+  const int fr = lane % 16, fg = lane / 16;  // fragment row and k-group of this lane
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload((kt + 1) * BK);
+    const uint8_t* As = smem + cur * kStageBytes;
+    const uint8_t* Bs = As + BM * BK;
+    i32x8 bf[kNJ];
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+      const int row = wn * WN + j * 16 + fr;
+      bf[j] = join(*reinterpret_cast<const i32x4*>(Bs + swizzle(row, 2 * fg)),
+                   *reinterpret_cast<const i32x4*>(Bs + swizzle(row, 2 * fg + 1)));
+    }
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+      const int row = wm * WM + i * 16 + fr;
+      const i32x8 af = join(*reinterpret_cast<const i32x4*>(As + swizzle(row, 2 * fg)),
+                            *reinterpret_cast<const i32x4*>(As + swizzle(row, 2 * fg + 1)));
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) acc[i][j] = mfma_e4m3(af, bf[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) swrite(cur ^ 1);
+    __syncthreads();
+  }
+
+  // Epilogue: lane holds rows 4*fg..4*fg+3 of column fr in every 16x16 block.  Stores go
+  // through a descriptor covering this tile's rows; columns past N get an out-of-range
+  // offset and are dropped.
+  const __amdgpu_buffer_rsrc_t ob = make_rsrc(out + (size_t)m0 * N, (size_t)rows_a * N * 2);
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int gn = n0 + wn * WN + j * 16 + fr;
+    const float bv = gn < N ? bf16_to_f32(bias[gn]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < kMI; ++i) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = wm * WM + i * 16 + 4 * fg + r;
+        const unsigned off = gn < N ? (unsigned)(row * N + gn) * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_rne(acc[i][j][r] * inv_scale + bv), ob, off, 0, 0);
+      }
+    }
+  }
+}
+
+constexpr int kSlotsPerInst = 64;  // a direct-to-LDS instruction writes 64 x 16 bytes
+
+// ---------------------------------------------------------------------------------------
+// Ring kernel: direct-to-LDS loads kStages-1 K-steps ahead (K % 16 == 0, 16-byte aligned)
+//
+// 256x256 output tile, 4 waves of 128x128, K in steps of 64 held in a ring of kStages
+// LDS stages of 32 KiB, so the copy of step k+kStages-1 is in flight while step k feeds
+// the MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4: lane l supplies 32 consecutive k of row
+// l % 32 starting at k = 32*(l/32); D register r of lane l is row 8*(r/4) + 4*(l/32) +
+// r%4, column l % 32).  W is fed as the A operand and x as the B operand, so D is the
+// transposed output block: lane l owns output row l % 32 and, per group of four
+// registers, four consecutive output columns, which it stores as one 8-byte bf16x4.
+// Rows of a tile are 64 bytes (four 16-byte chunks); chunk c of row r is stored at chunk
+// c ^ ((r >> 2) & 3) so the 16 rows one fragment read touches land in distinct banks.
+// ---------------------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int RBK = 64;
+constexpr int kRingStageBytes = (BM + BN) * RBK;  // 32 KiB
+constexpr int kRingDmaPerWave = (BM * RBK / 16) / kSlotsPerInst / (kThreads / kWave);  // 4
+
+__device__ __forceinline__ f32x16 mfma32_e4m3(i32x8 a, i32x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, kScaleOne, 0, kScaleOne);
+}
+
+__device__ __forceinline__ int swizzle64(int row, int chunk) {
+  return row * RBK + ((chunk ^ ((row >> 2) & 3)) << 4);
+}
+
+__device__ __forceinline__ void dma_tile64(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows,
+                                           int K, int k0, int wave, int lane) {
+  const int r16 = lane / 4, logical = (lane % 4) ^ ((r16 >> 2) & 3);
+  const int gk = k0 + 16 * logical;
+#pragma unroll
+  for (int i = 0; i < kRingDmaPerWave; ++i) {
+    const int group = wave * kRingDmaPerWave + i;  // 16 rows per instruction
+    const int row = group * 16 + r16;
+    const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off,
+        0, 0, 0);
+  }
+}
+
+// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9 encoding).
+template <int n>
+__device__ __forceinline__ void wait_vmcnt() {
+  __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// Epilogue of the ring kernel.  acc[i][j] is the transposed 32x32 block (output rows
+// i*32.., columns j*32.. of this wave's tile): lane l holds output row l % 32 and, in
+// registers 4q..4q+3, columns 8q + 4*(l/32) + 0..3.  With kVec4 (N % 4 == 0) those four
+// columns go out as one 8-byte store; otherwise one 2-byte store each.  Columns past N
+// get an out-of-range offset and are dropped by the buffer descriptor.
+template <bool kVec4>
+__device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4], uint16_t* out,
+                                                       const uint16_t* bias, int M, int N, int m0,
+                                                       int n0, int wm, int wn, int fr, int fg,
+                                                       int rows_a, float inv_scale) {
+  const __amdgpu_buffer_rsrc_t ob = make_rsrc(out + (size_t)m0 * N, (size_t)rows_a * N * 2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int gn = n0 + wn * WN + j * 32 + 8 * q + 4 * fg;  // first of four columns
+      float bv[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bv[e] = gn + e < N ? bf16_to_f32(bias[gn + e]) : 0.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = wm * WM + i * 32 + fr;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_rne(acc[i][j][4 * q + e] * inv_scale + bv[e]);
+        if constexpr (kVec4) {
+          const unsigned off = gn < N ? (unsigned)(row * N + gn) * 2u : kOutOfRange;
+          const i32x2 v = {(int)((unsigned)h[0] | ((unsigned)h[1] << 16)),
+                           (int)((unsigned)h[2] | ((unsigned)h[3] << 16))};
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, v), ob, off, 0, 0);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const unsigned off = gn + e < N ? (unsigned)(row * N + gn + e) * 2u : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b16(h[e], ob, off, 0, 0);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int kStages, bool kVec4Out>
+__global__ __launch_bounds__(kThreads) void fp8_gemm_ring(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
+    float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
+  static_assert(kStages >= 2 && kStages <= 5, "ring depth");
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+  int mt, nt;
+  tile_of(blockIdx.x, tm, tn, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int rows_a = min(BM, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t xa = make_rsrc(x + (size_t)m0 * K, (size_t)rows_a * K);
+  const __amdgpu_buffer_rsrc_t wb = make_rsrc(w + (size_t)n0 * K, (size_t)rows_b * K);
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int nk = (K + RBK - 1) / RBK;
+  auto issue = [&](int step) {
+    uint8_t* st = smem + (step % kStages) * kRingStageBytes;
+    dma_tile64(xa, st, rows_a, K, step * RBK, wave, lane);
+    dma_tile64(wb, st + BM * RBK, rows_b, K, step * RBK, wave, lane);
+  };
+#pragma unroll
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < nk) issue(s);
+
+  const int fr = lane % 32, fg = lane / 32;
+  constexpr int kPerStep = 2 * kRingDmaPerWave;  // DMA instructions per wave per step
+  for (int kt = 0; kt < nk; ++kt) {
+    // Step kt has landed once at most `pending` later steps' copies are outstanding.
+    const int pending = min(kStages - 2, nk - 1 - kt);
+    if (pending >= 3) wait_vmcnt<3 * kPerStep>();
+    else if (pending == 2) wait_vmcnt<2 * kPerStep>();
+    else if (pending == 1) wait_vmcnt<kPerStep>();
+    else wait_vmcnt<0>();
+    __syncthreads();  // all waves' copies of step kt landed; step kt-1's slot is free
+    if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
+
+    const uint8_t* As = smem + (kt % kStages) * kRingStageBytes;
+    const uint8_t* Bs = As + BM * RBK;
+    i32x8 bf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = wn * WN + j * 32 + fr;
+      bf[j] = join(*reinterpret_cast<const i32x4*>(Bs + swizzle64(row, 2 * fg)),
+                   *reinterpret_cast<const i32x4*>(Bs + swizzle64(row, 2 * fg + 1)));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = wm * WM + i * 32 + fr;
+      const i32x8 af = join(*reinterpret_cast<const i32x4*>(As + swizzle64(row, 2 * fg)),
+                            *reinterpret_cast<const i32x4*>(As + swizzle64(row, 2 * fg + 1)));
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(bf[j], af, acc[i][j]);
+    }
+  }
+  store_transposed_block<kVec4Out>(acc, out, bias, M, N, m0, n0, wm, wn, fr, fg, rows_a, inv_scale);
+}
+
+// ---------------------------------------------------------------------------------------
+// Skinny kernel (M <= 64)
+// ---------------------------------------------------------------------------------------
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyThreads = kSkinnyWaves * kWave;
+constexpr int kSkinnyMaxM = 64;
+
+template <int kVec>
+__global__ __launch_bounds__(kSkinnyThreads) void fp8_gemm_skinny(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
+    float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
+  __shared__ float part[kSkinnyWaves][kSkinnyMaxM][16];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int n0 = blockIdx.x * 16;
+  const int fr = lane % 16, fg = lane / 16;
+  const int rblocks = (M + 15) / 16;
+  const int steps = (K + 127) / 128;
+  const int per_wave = (steps + kSkinnyWaves - 1) / kSkinnyWaves;
+  const int s0 = wave * per_wave, s1 = min(steps, s0 + per_wave);
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int rows_w = min(16, N - n0);
+  const __amdgpu_buffer_rsrc_t wb = make_rsrc(w + (size_t)n0 * K, (size_t)rows_w * K);
+  const __amdgpu_buffer_rsrc_t xa = make_rsrc(x, (size_t)M * K);
+  const unsigned woff = fr < rows_w ? (unsigned)(fr * K) : kOutOfRange;
+  for (int s = s0; s < s1; ++s) {
+    const int k = s * 128 + 32 * fg;
+    const unsigned wo = woff == kOutOfRange ? kOutOfRange : woff + k;
+    const i32x8 bf = join(load16<kVec>(wb, wo, k, K), load16<kVec>(wb, wo + 16, k + 16, K));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i < rblocks) {
+        const int gm = i * 16 + fr;
+        const unsigned xo = gm < M ? (unsigned)(gm * K + k) : kOutOfRange;
+        const i32x8 af = join(load16<kVec>(xa, xo, k, K), load16<kVec>(xa, xo + 16, k + 16, K));
+        acc[i] = mfma_e4m3(af, bf, acc[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (i < rblocks)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) part[wave][i * 16 + 4 * fg + r][fr] = acc[i][r];
+  __syncthreads();
+  for (int e = threadIdx.x; e < M * 16; e += kSkinnyThreads) {
+    const int m = e / 16, c = e % 16;
+    const int n = n0 + c;
+    if (n >= N) continue;
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < kSkinnyWaves; ++v) s += part[v][m][c];
+    out[(size_t)m * N + n] = f32_to_bf16_rne(s * inv_scale + bf16_to_f32(bias[n]));
+  }
+}
+
+inline int vec_width(const uint8_t* x, const uint8_t* w, int K) {
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w);
+  if (K % 16 == 0 && (bits & 15) == 0) return 16;
+  if (K % 8 == 0 && (bits & 7) == 0) return 8;
+  return 1;
+}
+
+}  // namespace fp8
+}  // namespace taskops
