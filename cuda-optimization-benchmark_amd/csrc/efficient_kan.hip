@@ -1,24 +1,24 @@
 // efficient_kan on gfx950: KANLinear forward.
 //
-// Op: tasks/efficient_kan/reference.py:33-51 (fp64 oracle :54-57); drop-in signature
-// tasks/efficient_kan/tests/task.json:3, replacing reference/efficient_kan/solution.cu:177-288.
-//
-// Row-per-workgroup version: the expanded activation row [silu(x_i), B_0(x_i) ..
-// B_{C-1}(x_i)] is built in LDS feature-chunk by feature-chunk with the Cox-de Boor
-// recurrence, and each thread accumulates one output column in fp32.
-#include "common.hpp"
+// Drop-in signature tasks/efficient_kan/tests/task.json:3, replacing
+// reference/efficient_kan/solution.cu:177-288.  Fast path (efficient_kan.hpp): spline
+// order 3 with at most 16 bases per feature — a weight-preparation launch and one fused
+// fp16x3 MFMA GEMM.  Other shapes take the row-wise fp32 path below.
+#include "efficient_kan.hpp"
 
 namespace taskops {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kFeat = 128;     // features per LDS chunk
-constexpr int kMaxKnots = 32;  // grid_size + 2*spline_order + 1
-constexpr int kMaxC = kMaxKnots - 1;
+constexpr int kStages = 4;
 
-// Cox-de Boor on one feature's knot row: order-0 indicators, then spline_order rounds.
-__device__ void bsplines(const float* __restrict__ g, int L, int order, float x, float* out) {
-  float b[kMaxKnots];
+// Row-wise fp32 path for shapes outside the fast path: the expanded activation row is
+// built in LDS with the Cox-de Boor recurrence, one output column per thread.
+constexpr int kRowThreads = 256;
+constexpr int kFeat = 128;
+constexpr int kMaxKnotsRow = 32;
+
+__device__ void bsplines_full(const float* __restrict__ g, int L, int order, float x, float* out) {
+  float b[kMaxKnotsRow];
   for (int j = 0; j < L - 1; ++j) b[j] = (x >= g[j] && x < g[j + 1]) ? 1.0f : 0.0f;
   for (int k = 1; k <= order; ++k) {
     for (int j = 0; j < L - 1 - k; ++j) {
@@ -30,35 +30,65 @@ __device__ void bsplines(const float* __restrict__ g, int L, int order, float x,
   for (int c = 0; c < L - 1 - order; ++c) out[c] = b[c];
 }
 
-__global__ __launch_bounds__(kThreads) void kan_rowwise(
+__global__ __launch_bounds__(kRowThreads) void kan_rowwise(
     const float* __restrict__ x, const float* __restrict__ grid, const float* __restrict__ wb,
     const float* __restrict__ ws, const float* __restrict__ sc, int G, int order, int I, int O,
     float* __restrict__ out) {
   extern __shared__ float lds[];  // [kFeat][1 + C]
   const int L = G + 2 * order + 1, C = G + order, S = 1 + C;
   const int b = blockIdx.y;
-  const int o = blockIdx.x * kThreads + threadIdx.x;
+  const int o = blockIdx.x * kRowThreads + threadIdx.x;
   float acc = 0.0f;
   for (int i0 = 0; i0 < I; i0 += kFeat) {
     const int nf = min(kFeat, I - i0);
     __syncthreads();
-    for (int f = threadIdx.x; f < nf; f += kThreads) {
+    for (int f = threadIdx.x; f < nf; f += kRowThreads) {
       const float xv = x[(size_t)b * I + i0 + f];
       lds[f * S] = xv / (1.0f + expf(-xv));
-      bsplines(grid + (size_t)(i0 + f) * L, L, order, xv, lds + f * S + 1);
+      bsplines_full(grid + (size_t)(i0 + f) * L, L, order, xv, lds + f * S + 1);
     }
     __syncthreads();
     if (o < O) {
       for (int f = 0; f < nf; ++f) {
         const size_t oi = (size_t)o * I + i0 + f;
-        float s = lds[f * S] * wb[oi];
         float t = 0.0f;
         for (int c = 0; c < C; ++c) t = fmaf(lds[f * S + 1 + c], ws[oi * C + c], t);
-        acc += s + t * sc[oi];
+        acc += lds[f * S] * wb[oi] + t * sc[oi];
       }
     }
   }
   if (o < O) out[(size_t)b * O + o] = acc;
+}
+
+template <int kCp>
+hipError_t launch_fast(const float* x, const float* grid, const float* wb, const float* ws,
+                       const float* sc, int C, int B, int I, int O, int L, float* out,
+                       hipStream_t stream) {
+  using namespace kan;
+  const int ngroups = (I + kGroup - 1) / kGroup;
+  const int Opad = ((O + BN - 1) / BN) * BN;
+  const int nq = ngroups * (1 + kCp);
+  const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
+  void* wsp = nullptr;
+  hipError_t e = workspace(kSlotKan, 2 * half_bytes + (size_t)Opad * sizeof(float), stream, &wsp);
+  if (e != hipSuccess) return e;
+  auto* bhi = static_cast<_Float16*>(wsp);
+  auto* blo = reinterpret_cast<_Float16*>(static_cast<char*>(wsp) + half_bytes);
+  auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
+  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, kCp, ngroups,
+                     Opad, bhi, blo, colscale);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
+  const size_t lds = (size_t)kStages * kStageBytes + kKnotBytes;
+  const bool vec4 = (O % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+  if (vec4)
+    hipLaunchKernelGGL((kan_gemm<kCp, kStages, true>), dim3(tiles), dim3(kThreads), lds, stream, x, grid,
+                       B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+  else
+    hipLaunchKernelGGL((kan_gemm<kCp, kStages, false>), dim3(tiles), dim3(kThreads), lds, stream, x, grid,
+                       B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -72,11 +102,19 @@ extern "C" hipError_t taskops_efficient_kan(const float* x, const float* grid,
                                             int32_t spline_order, int32_t B, int32_t I, int32_t O,
                                             float* out, hipStream_t stream) {
   if (B < 0 || I < 0 || O < 0 || grid_size < 1 || spline_order < 0) return hipErrorInvalidValue;
-  if (grid_size + 2 * spline_order + 1 > kMaxKnots) return hipErrorInvalidValue;
+  const int L = grid_size + 2 * spline_order + 1;
+  if (L > kMaxKnotsRow) return hipErrorInvalidValue;
   if (B == 0 || O == 0) return hipSuccess;
-  const int S = 1 + grid_size + spline_order;
-  dim3 g((O + kThreads - 1) / kThreads, B);
-  hipLaunchKernelGGL(kan_rowwise, g, dim3(kThreads), (size_t)kFeat * S * sizeof(float), stream, x,
+  const int C = grid_size + spline_order;
+  const int Cp = kan::padded_bases(C);
+  if (spline_order == kan::kOrder && I > 0 && L <= kan::kMaxKnots && (Cp == 8 || Cp == 16)) {
+    if (Cp == 8)
+      return launch_fast<8>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
+    return launch_fast<16>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
+  }
+  const int S = 1 + C;
+  dim3 g((O + kRowThreads - 1) / kRowThreads, B);
+  hipLaunchKernelGGL(kan_rowwise, g, dim3(kRowThreads), (size_t)kFeat * S * sizeof(float), stream, x,
                      grid, base_weight, spline_weight, spline_scaler, (int)grid_size,
                      (int)spline_order, (int)I, (int)O, out);
   return hipGetLastError();
