@@ -12,8 +12,10 @@
 // The product is accumulated in fp32 and the epilogue applies 1/(sx*sw), adds the bf16
 // bias and rounds to bf16 (nearest-even) once.
 //
-// Two kernels, one launch per call:
-//  * tiled (M > 64): 256x256 output tile per workgroup of 4 waves (one per SIMD, each
+// Three kernels, one launch per call:
+//  * ring (M > 64, K % 16 == 0, 16-byte aligned operands): the main path, described at
+//    fp8_gemm_ring below — direct-to-LDS copies several K-steps ahead, 32x32x64 MFMAs.
+//  * tiled (M > 64, other K or alignment): 256x256 output tile per workgroup of 4 waves (one per SIMD, each
 //    128x128 = 8x8 MFMA blocks whose 256 fp32 accumulators sit in AGPRs), K in steps of
 //    128 staged through LDS (2 stages x 64 KiB, 16-byte
 //    chunks XOR-swizzled by row so a wave's fragment reads spread over the banks).  The

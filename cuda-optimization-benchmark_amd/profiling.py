@@ -1,0 +1,159 @@
+"""Summaries of rocprofv3 result databases, for the text files kept under profiles/.
+
+    python cuda-optimization-benchmark_amd/profiling.py stats DIR
+        Per-kernel dispatch count and average / median / min / max duration from a
+        `rocprofv3 --kernel-trace --stats -d DIR` run (a markdown table).
+
+    python cuda-optimization-benchmark_amd/profiling.py traffic FETCH_DIR WRITE_DIR [--json OUT]
+        Per-kernel HBM traffic per dispatch from two `rocprofv3 --pmc FETCH_SIZE` and
+        `--pmc WRITE_SIZE` runs of `bench.py --copy-probe`.  Both counters (KiB per
+        dispatch) are scaled by what they read for the probe's plain device copy of
+        bench.COPY_PROBE_BYTES, so a copy of n bytes reads exactly n fetched and n written.
+        With --json, writes {bench op key: bytes per launch of its dominant kernel}.
+
+Only the standard library is used: the databases are SQLite files.
+"""
+from __future__ import annotations
+
+import argparse
+import collections
+import glob
+import json
+import sqlite3
+import statistics
+import sys
+
+# Dominant kernel of each bench workload (a substring of the mangled kernel name).
+DOMINANT = {
+    "reward_to_go": "reward_to_go_kernel",
+    "pow_abs_sqrt_mean": "pow_abs_sqrt_mean_kernel",
+    "leaky": "leaky_kernel",
+    "ppo_clip": "ppo_clip_kernel",
+    "efficient_kan": "kan_gemm",
+    "fp8_linear": "fp8_gemm_ring",
+    "fp8_linear_m16": "fp8_gemm_skinny",
+}
+COPY_PROBE_BYTES = 256 << 20
+
+
+def _db(d: str) -> sqlite3.Connection:
+    files = sorted(glob.glob(f"{d}/**/*results.db", recursive=True))
+    if not files:
+        raise SystemExit(f"no *results.db under {d}")
+    return sqlite3.connect(files[0])
+
+
+def kernel_stats(d: str) -> dict:
+    c = _db(d)
+    agg = collections.defaultdict(list)
+    for name, dur in c.execute("select name, duration from kernels"):
+        agg[name].append(dur / 1e3)
+    return agg
+
+
+def _short(name: str, width: int = 72) -> str:
+    return name if len(name) <= width else name[: width - 3] + "..."
+
+
+def print_stats(d: str) -> None:
+    agg = kernel_stats(d)
+    print("| kernel | calls | avg us | median us | min us | max us |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for k, v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{_short(k)}` | {len(v)} | {statistics.mean(v):.2f} | {statistics.median(v):.2f} "
+              f"| {min(v):.2f} | {max(v):.2f} |")
+
+
+def counter_values(d: str, counter: str) -> dict:
+    """kernel name -> per-dispatch counter values (summed over the counter's instances),
+    in dispatch order."""
+    c = _db(d)
+    per = collections.defaultdict(float)
+    names = {}
+    for name, disp, val in c.execute(
+            "select kernel_name, dispatch_id, value from counters_collection where counter_name = ?",
+            (counter,)):
+        per[disp] += val
+        names[disp] = name
+    agg = collections.defaultdict(list)
+    for disp in sorted(per):
+        agg[names[disp]].append(per[disp])
+    return agg
+
+
+def _copy_calibration(vals: dict) -> tuple[str, float]:
+    """The probe's copies: the three largest dispatches of a copy kernel (the probe's
+    256 MiB copies are the largest copies in a bench run), which must agree within 1%."""
+    cands = sorted(((v, k) for k, vs in vals.items() if "copy" in k.lower() for v in vs), reverse=True)
+    if len(cands) < 3:
+        raise SystemExit("no copy probe found: run bench.py with --copy-probe")
+    top = [v for v, _ in cands[:3]]
+    if max(top) > 1.01 * min(top):
+        raise SystemExit(f"copy probe dispatches disagree: {top}")
+    return cands[0][1], statistics.mean(top)
+
+
+def traffic(fetch_dir: str, write_dir: str) -> dict:
+    f = counter_values(fetch_dir, "FETCH_SIZE")
+    w = counter_values(write_dir, "WRITE_SIZE")
+    fk, fv = _copy_calibration(f)
+    _, wv = _copy_calibration(w)
+    ff = COPY_PROBE_BYTES / fv   # bytes per counter unit, from the copy
+    wf = COPY_PROBE_BYTES / wv
+    rows = {}
+    for k in sorted(set(f) | set(w)):
+        n = len(f.get(k) or w.get(k))
+        rows[k] = {"dispatches": n,
+                   "fetch_bytes": statistics.mean(f[k]) * ff if k in f else None,
+                   "write_bytes": statistics.mean(w[k]) * wf if k in w else None}
+    return {"copy_kernel": fk, "fetch_factor": ff, "write_factor": wf,
+            "copy_fetch_kib": fv, "copy_write_kib": wv, "kernels": rows}
+
+
+def print_traffic(t: dict) -> None:
+    print(f"Calibration: `{_short(t['copy_kernel'])}` copying {COPY_PROBE_BYTES} bytes reads "
+          f"FETCH_SIZE {t['copy_fetch_kib']:.1f} and WRITE_SIZE {t['copy_write_kib']:.1f} per dispatch; "
+          f"factors {t['fetch_factor']:.2f} and {t['write_factor']:.2f} bytes per unit.\n")
+    print("| kernel | dispatches | fetched MB / launch | written MB / launch | total MB |")
+    print("|---|---:|---:|---:|---:|")
+    for k, r in t["kernels"].items():
+        fb, wb = r["fetch_bytes"] or 0.0, r["write_bytes"] or 0.0
+        print(f"| `{_short(k)}` | {r['dispatches']} | {fb / 1e6:.2f} | {wb / 1e6:.2f} | {(fb + wb) / 1e6:.2f} |")
+
+
+def dominant_traffic(t: dict) -> dict:
+    out = {}
+    for op, sub in DOMINANT.items():
+        hits = [r for k, r in t["kernels"].items() if sub in k and "copy" not in k.lower()]
+        if not hits:
+            continue
+        fb = statistics.mean(r["fetch_bytes"] or 0.0 for r in hits)
+        wb = statistics.mean(r["write_bytes"] or 0.0 for r in hits)
+        out[op] = int(round(fb + wb))
+    return out
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_dir")
+    t.add_argument("write_dir")
+    t.add_argument("--json")
+    a = ap.parse_args(argv)
+    if a.cmd == "stats":
+        print_stats(a.dir)
+    else:
+        tr = traffic(a.fetch_dir, a.write_dir)
+        print_traffic(tr)
+        if a.json:
+            with open(a.json, "w") as fh:
+                json.dump(dominant_traffic(tr), fh, indent=1, sort_keys=True)
+                fh.write("\n")
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

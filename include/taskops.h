@@ -10,7 +10,7 @@
  *     reference's prompts require: "Launch your work on the default stream");
  *   - a return value: hipSuccess (0) or the hipError_t of the failed launch or argument
  *     check.  The reference's `void` entry has no error channel (errors surface at the
- *     caller's next synchronize); the C++ drop-in overloads in dropin.hip keep `void`.
+ *     caller's next synchronize); the C++ drop-in overloads in dropin.hpp keep `void`.
  *
  * All pointers are device pointers to contiguous row-major data, owned by the caller.
  * The library keeps one small cached workspace per device (allocated on the first call

@@ -88,6 +88,38 @@ def test_baseline_efficient_kan_rows(lib):
     assert s["bad"] == 0, s
 
 
+# (B, I, O, grid_size, spline_order, x_range, non-uniform knots).  Order 3 with at most 16
+# knots per feature runs the fused fp16x3 MFMA kernel (C = 4, 8, 11, 12 cover both padded
+# basis widths); the others run the row-wise fp32 kernel.  Ragged B, I and O exercise every
+# tile tail; x_range > 1 puts inputs outside the knot span.
+KAN_SHAPES = [
+    (130, 45, 70, 5, 3, 1.5, False),
+    (67, 33, 258, 9, 3, 1.0, True),
+    (40, 20, 36, 8, 3, 2.0, False),
+    (9, 30, 31, 1, 3, 1.0, False),
+    (33, 17, 19, 10, 3, 1.0, False),
+    (21, 40, 50, 6, 2, 1.2, True),
+    (16, 12, 8, 13, 1, 1.0, False),
+]
+
+
+@pytest.mark.parametrize("shape", KAN_SHAPES, ids=[f"B{s[0]}_I{s[1]}_O{s[2]}_G{s[3]}_K{s[4]}" for s in KAN_SHAPES])
+def test_efficient_kan_shapes(lib, shape):
+    B, I, O, G, K, xr, nonuniform = shape
+    print(f"\n[parity] efficient_kan {shape}", flush=True)
+    case = dict(name="k", seed=900 + B, B=B, I=I, O=O, grid_size=G, spline_order=K, x_range=xr)
+    inp = inputs.make_inputs("efficient_kan", case)
+    if nonuniform:
+        g = torch.Generator().manual_seed(B)
+        L = G + 2 * K + 1
+        inp["grid"] = torch.sort(torch.rand(I, L, generator=g) * 3.0 - 1.5, dim=1).values.contiguous()
+    want = exact.efficient_kan(inp)["out"]
+    for _ in range(2):
+        got = capi.run_op(lib, "efficient_kan", inp)["out"].cpu().numpy()
+        s = compare(got, want, tasks.load_task("efficient_kan")["tolerance"])
+        assert s["bad"] == 0, s
+
+
 @pytest.mark.parametrize("key", ["fp8_linear", "fp8_linear_m16"])
 def test_baseline_fp8_rows(lib, key):
     print(f"\n[parity] baseline {key}", flush=True)
