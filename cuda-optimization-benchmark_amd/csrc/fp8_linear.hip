@@ -2,16 +2,13 @@
 //
 // Drop-in signature tasks/fp8_linear/tests/task.json:3, replacing
 // reference/fp8_linear/solution.cu:276-321.  Kernels are in fp8_linear.hpp: the skinny
-// split-K kernel for M <= 64, the ring (direct-to-LDS, multi-stage) kernel when K % 16 == 0
-// and the operands are 16-byte aligned, and the register-staged tiled kernel otherwise.
+// split-K kernel for M <= 64, the wide (direct-to-LDS, 128-byte rows) kernel when
+// K % 16 == 0 and the operands are 16-byte aligned, and the register-staged tiled kernel
+// otherwise.
 #include "fp8_linear.hpp"
 
 using namespace taskops;
 using namespace taskops::fp8;
-
-namespace {
-constexpr int kRingStages = 4;
-}  // namespace
 
 extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_fp8,
                                          float scale_x, const uint8_t* w_fp8, float scale_w,
@@ -37,19 +34,20 @@ extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const 
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const size_t lds = 2 * kStageBytes;
   if (vec == 16) {
-    const size_t ring_lds = (size_t)kRingStages * kRingStageBytes;
-    if (N % 4 == 0 && (reinterpret_cast<uintptr_t>(output) & 7) == 0)
-      hipLaunchKernelGGL((fp8_gemm_ring<kRingStages, true>), dim3(tiles), dim3(kThreads), ring_lds,
-                         stream, x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+    const size_t wide_lds = 2 * (size_t)kWideStageBytes + kBiasBytes;
+    const uintptr_t o = reinterpret_cast<uintptr_t>(output);
+    if (N % 8 == 0 && (o & 15) == 0)
+      hipLaunchKernelGGL(fp8_gemm_wide<2>, dim3(tiles), dim3(kThreads), wide_lds, stream, x_fp8, w_fp8,
+                         (int)M, (int)N, (int)K, inv, bias, output);
+    else if (N % 4 == 0 && (o & 7) == 0)
+      hipLaunchKernelGGL(fp8_gemm_wide<1>, dim3(tiles), dim3(kThreads), wide_lds, stream, x_fp8, w_fp8,
+                         (int)M, (int)N, (int)K, inv, bias, output);
     else
-      hipLaunchKernelGGL((fp8_gemm_ring<kRingStages, false>), dim3(tiles), dim3(kThreads), ring_lds,
-                         stream, x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+      hipLaunchKernelGGL(fp8_gemm_wide<0>, dim3(tiles), dim3(kThreads), wide_lds, stream, x_fp8, w_fp8,
+                         (int)M, (int)N, (int)K, inv, bias, output);
     return hipGetLastError();
   }
-  if (vec == 16)
-    hipLaunchKernelGGL(fp8_gemm_tiled<16>, dim3(tiles), dim3(kThreads), lds, stream, x_fp8, w_fp8,
-                       (int)M, (int)N, (int)K, inv, bias, output);
-  else if (vec == 8)
+  if (vec == 8)
     hipLaunchKernelGGL(fp8_gemm_tiled<8>, dim3(tiles), dim3(kThreads), lds, stream, x_fp8, w_fp8,
                        (int)M, (int)N, (int)K, inv, bias, output);
   else

@@ -13,8 +13,9 @@
 // bias and rounds to bf16 (nearest-even) once.
 //
 // Three kernels, one launch per call:
-//  * ring (M > 64, K % 16 == 0, 16-byte aligned operands): the main path, described at
-//    fp8_gemm_ring below — direct-to-LDS copies several K-steps ahead, 32x32x64 MFMAs.
+//  * wide (M > 64, K % 16 == 0, 16-byte aligned operands): the main path, described at
+//    fp8_gemm_wide below — direct-to-LDS copies of whole 128-byte row segments into two
+//    64 KiB stages, 32x32x64 MFMAs with fragments read a half-step ahead.
 //  * tiled (M > 64, other K or alignment): 256x256 output tile per workgroup of 4 waves (one per SIMD, each
 //    128x128 = 8x8 MFMA blocks whose 256 fp32 accumulators sit in AGPRs), K in steps of
 //    128 staged through LDS (2 stages x 64 KiB, 16-byte
@@ -51,6 +52,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((unsigned)b << 16); }
+
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats to two bf16 (round to nearest even) packed low-first: one
+// v_cvt_pk_bf16_f32 on gfx950.
+__device__ __forceinline__ unsigned pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
+}
 
 // Buffer resources: a 128-bit descriptor (base, byte size) makes the hardware return zero
 // for loads past the size and drop stores past it, so tile tails need no branches.
@@ -204,11 +214,19 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_tiled(
   // Epilogue: lane holds rows 4*fg..4*fg+3 of column fr in every 16x16 block.  Stores go
   // through a descriptor covering this tile's rows; columns past N get an out-of-range
   // offset and are dropped.
+  // All bias loads are issued before the first store: vmcnt also counts stores, so a load
+  // between stores would wait for every earlier store to complete.
   const __amdgpu_buffer_rsrc_t ob = make_rsrc(out + (size_t)m0 * N, (size_t)rows_a * N * 2);
+  float bvs[kNJ];
 #pragma unroll
   for (int j = 0; j < kNJ; ++j) {
     const int gn = n0 + wn * WN + j * 16 + fr;
-    const float bv = gn < N ? bf16_to_f32(bias[gn]) : 0.0f;
+    bvs[j] = gn < N ? bf16_to_f32(bias[gn]) : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int gn = n0 + wn * WN + j * 16 + fr;
+    const float bv = bvs[j];
 #pragma unroll
     for (int i = 0; i < kMI; ++i) {
 #pragma unroll
@@ -224,45 +242,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_tiled(
 constexpr int kSlotsPerInst = 64;  // a direct-to-LDS instruction writes 64 x 16 bytes
 
 // ---------------------------------------------------------------------------------------
-// Ring kernel: direct-to-LDS loads kStages-1 K-steps ahead (K % 16 == 0, 16-byte aligned)
-//
-// 256x256 output tile, 4 waves of 128x128, K in steps of 64 held in a ring of kStages
-// LDS stages of 32 KiB, so the copy of step k+kStages-1 is in flight while step k feeds
-// the MFMAs (v_mfma_scale_f32_32x32x64_f8f6f4: lane l supplies 32 consecutive k of row
-// l % 32 starting at k = 32*(l/32); D register r of lane l is row 8*(r/4) + 4*(l/32) +
-// r%4, column l % 32).  W is fed as the A operand and x as the B operand, so D is the
-// transposed output block: lane l owns output row l % 32 and, per group of four
-// registers, four consecutive output columns, which it stores as one 8-byte bf16x4.
-// Rows of a tile are 64 bytes (four 16-byte chunks); chunk c of row r is stored at chunk
-// c ^ ((r >> 2) & 3) so the 16 rows one fragment read touches land in distinct banks.
+// Shared pieces of the wide kernel: 32x32x64 MFMA, vmcnt waits, epilogues, bias staging.
 // ---------------------------------------------------------------------------------------
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int RBK = 64;
-constexpr int kRingStageBytes = (BM + BN) * RBK;  // 32 KiB
-constexpr int kRingDmaPerWave = (BM * RBK / 16) / kSlotsPerInst / (kThreads / kWave);  // 4
-
+// v_mfma_scale_f32_32x32x64_f8f6f4: lane l supplies 32 consecutive k of row l % 32
+// starting at k = 32*(l/32); D register r of lane l is row 8*(r/4) + 4*(l/32) + r%4,
+// column l % 32.
 __device__ __forceinline__ f32x16 mfma32_e4m3(i32x8 a, i32x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, c, 0, 0, 0, kScaleOne, 0, kScaleOne);
-}
-
-__device__ __forceinline__ int swizzle64(int row, int chunk) {
-  return row * RBK + ((chunk ^ ((row >> 2) & 3)) << 4);
-}
-
-__device__ __forceinline__ void dma_tile64(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows,
-                                           int K, int k0, int wave, int lane) {
-  const int r16 = lane / 4, logical = (lane % 4) ^ ((r16 >> 2) & 3);
-  const int gk = k0 + 16 * logical;
-#pragma unroll
-  for (int i = 0; i < kRingDmaPerWave; ++i) {
-    const int group = wave * kRingDmaPerWave + i;  // 16 rows per instruction
-    const int row = group * 16 + r16;
-    const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off,
-        0, 0, 0);
-  }
 }
 
 // s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9 encoding).
@@ -271,14 +259,15 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// Epilogue of the ring kernel.  acc[i][j] is the transposed 32x32 block (output rows
+// Direct epilogue of the wide kernel.  acc[i][j] is the transposed 32x32 block (output rows
 // i*32.., columns j*32.. of this wave's tile): lane l holds output row l % 32 and, in
 // registers 4q..4q+3, columns 8q + 4*(l/32) + 0..3.  With kVec4 (N % 4 == 0) those four
 // columns go out as one 8-byte store; otherwise one 2-byte store each.  Columns past N
-// get an out-of-range offset and are dropped by the buffer descriptor.
+// get an out-of-range offset and are dropped by the buffer descriptor.  bias_s holds the
+// tile's BN bias values in LDS (zero past N), so no global load sits between the stores.
 template <bool kVec4>
 __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4], uint16_t* out,
-                                                       const uint16_t* bias, int M, int N, int m0,
+                                                       const uint16_t* bias_s, int N, int m0,
                                                        int n0, int wm, int wn, int fr, int fg,
                                                        int rows_a, float inv_scale) {
   const __amdgpu_buffer_rsrc_t ob = make_rsrc(out + (size_t)m0 * N, (size_t)rows_a * N * 2);
@@ -286,22 +275,25 @@ __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4]
   for (int j = 0; j < 4; ++j) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int gn = n0 + wn * WN + j * 32 + 8 * q + 4 * fg;  // first of four columns
-      float bv[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bv[e] = gn + e < N ? bf16_to_f32(bias[gn + e]) : 0.0f;
+      const int c = wn * WN + j * 32 + 8 * q + 4 * fg;  // first of four tile columns
+      const int gn = n0 + c;
+      const i32x2 braw = *reinterpret_cast<const i32x2*>(bias_s + c);
+      const float bv[4] = {__uint_as_float((unsigned)braw.x << 16), __uint_as_float((unsigned)braw.x & 0xffff0000u),
+                           __uint_as_float((unsigned)braw.y << 16), __uint_as_float((unsigned)braw.y & 0xffff0000u)};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = wm * WM + i * 32 + fr;
-        uint16_t h[4];
+        float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = f32_to_bf16_rne(acc[i][j][4 * q + e] * inv_scale + bv[e]);
+        for (int e = 0; e < 4; ++e) v[e] = fmaf(acc[i][j][4 * q + e], inv_scale, bv[e]);
+        const unsigned p01 = pack_bf16x2(v[0], v[1]), p23 = pack_bf16x2(v[2], v[3]);
         if constexpr (kVec4) {
           const unsigned off = gn < N ? (unsigned)(row * N + gn) * 2u : kOutOfRange;
-          const i32x2 v = {(int)((unsigned)h[0] | ((unsigned)h[1] << 16)),
-                           (int)((unsigned)h[2] | ((unsigned)h[3] << 16))};
-          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(__attribute__((ext_vector_type(2))) unsigned, v), ob, off, 0, 0);
+          typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{p01, p23}, ob, off, 0, 0);
         } else {
+          const unsigned short h[4] = {(unsigned short)p01, (unsigned short)(p01 >> 16),
+                                       (unsigned short)p23, (unsigned short)(p23 >> 16)};
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const unsigned off = gn + e < N ? (unsigned)(row * N + gn + e) * 2u : kOutOfRange;
@@ -313,11 +305,113 @@ __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4]
   }
 }
 
-template <int kStages, bool kVec4Out>
-__global__ __launch_bounds__(kThreads) void fp8_gemm_ring(
+// Epilogue through LDS (N % 8 == 0, 16-byte aligned output): the 256x256 bf16 tile is
+// assembled in `tile_s` (128 KiB, the two stages once every copy has landed and every
+// wave is past its last fragment read), then each store instruction writes two whole
+// 512-byte tile rows, instead of 16 bytes into each of 32 rows.  Tile row r's 16-byte
+// chunk c sits at chunk c ^ (r % 32), so both the column-wise writes and the row-wise
+// reads spread over all banks.
+constexpr int kTileRowBytes = BN * 2;  // 512
+__device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16_t* out,
+                                               const uint16_t* bias_s, uint8_t* tile_s, int N,
+                                               int m0, int n0, int wm, int wn, int fr, int fg,
+                                               int rows_a, int rows_b, float inv_scale, int tid) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = wn * WN + j * 32 + 8 * q + 4 * fg;  // first of four tile columns
+      const i32x2 braw = *reinterpret_cast<const i32x2*>(bias_s + c);
+      const float bv[4] = {__uint_as_float((unsigned)braw.x << 16), __uint_as_float((unsigned)braw.x & 0xffff0000u),
+                           __uint_as_float((unsigned)braw.y << 16), __uint_as_float((unsigned)braw.y & 0xffff0000u)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = wm * WM + i * 32 + fr;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = fmaf(acc[i][j][4 * q + e], inv_scale, bv[e]);
+        const int chunk = c / 8, half = (c / 4) & 1;
+        *reinterpret_cast<i32x2*>(tile_s + r * kTileRowBytes + ((chunk ^ (r & 31)) << 4) + 8 * half) =
+            i32x2{(int)pack_bf16x2(v[0], v[1]), (int)pack_bf16x2(v[2], v[3])};
+      }
+    }
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ob = make_rsrc(out + (size_t)m0 * N, (size_t)rows_a * N * 2);
+  const int lane = tid % kWave, wave = tid / kWave;
+  const int chunk = lane % 32;
+  const bool col_ok = chunk * 8 < rows_b;  // rows_b: valid columns of this tile (N % 8 == 0)
+#pragma unroll 4
+  for (int s = 0; s < BM / 2 / (kThreads / kWave); ++s) {
+    const int r = (wave * (BM / 2 / (kThreads / kWave)) + s) * 2 + lane / 32;
+    const i32x4 v = *reinterpret_cast<const i32x4*>(tile_s + r * kTileRowBytes + ((chunk ^ (r & 31)) << 4));
+    const unsigned off = (r < rows_a && col_ok) ? (unsigned)(r * N + n0 + chunk * 8) * 2u : kOutOfRange;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), ob, off, 0, 0);
+  }
+}
+
+// Bias staging for the wide kernel: thread t (kThreads == BN) loads bias[n0 + t] (zero
+// past N) before the prologue's copies, so the first copy wait covers it; the kernel then
+// writes it to LDS, where the epilogue reads it after a later barrier.
+static_assert(kThreads == BN, "one bias value per thread");
+static_assert(BM * kTileRowBytes <= 2 * (BM + BN) * 128, "the output tile fits the two stages");
+constexpr int kBiasBytes = BN * 2;
+__device__ __forceinline__ unsigned short load_bias(const uint16_t* bias, int n0, int rows_b, int tid) {
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + n0, (size_t)rows_b * 2);
+  return __builtin_amdgcn_raw_buffer_load_b16(rb, tid < rows_b ? (unsigned)tid * 2u : kOutOfRange, 0, 0);
+}
+
+
+// ---------------------------------------------------------------------------------------
+// Wide kernel (the main path: M > 64, K % 16 == 0, 16-byte aligned operands).
+//
+// 256x256 output tile, 4 waves of 128x128 (4x4 blocks of 32x32x64 MFMAs, accumulators in
+// AGPRs), W fed as the A operand so D is the transposed block.  The copy engine's rate is
+// set by requests, not bytes: measured on MI355X, a 128-byte run per row moves ~45% more
+// per clock than a 64-byte one, and deeper buffering does not help.  So K advances in
+// steps of 128 (each tile row is one whole 128-byte line) through two 64 KiB LDS stages.
+// Each step is two halves of 64 k (16 MFMAs per wave each); the fragments of the second
+// half are read while the first half's MFMAs run, and those of the next step's first half
+// while the second half's run, so a stage is free for the next copy as soon as every wave
+// has passed the mid-step barrier.  Row r's 16-byte chunk c sits at chunk c ^ ((r >> 1) &
+// 7), which spreads any 16 consecutive rows of one chunk over all banks.  Accumulation
+// order is k ascending in 64-wide MFMA steps, as in the tiled kernel's 128-wide steps of
+// two 64-wide halves.
+// ---------------------------------------------------------------------------------------
+constexpr int WBK = 128;
+constexpr int kWideStageBytes = (BM + BN) * WBK;                    // 64 KiB
+constexpr int kWideDmaPerWave = (BM * WBK / 16) / kSlotsPerInst / (kThreads / kWave);  // 8
+
+__device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
+
+__device__ __forceinline__ void dma_tile128(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows,
+                                            int K, int k0, int wave, int lane) {
+  const int r8 = lane / 8, p = lane % 8;  // row within the 8-row group, physical chunk
+#pragma unroll
+  for (int i = 0; i < kWideDmaPerWave; ++i) {
+    const int group = wave * kWideDmaPerWave + i;  // 8 rows per instruction
+    const int row = group * 8 + r8;
+    const int gk = k0 + 16 * (p ^ swz128(row));
+    const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off,
+        0, 0, 0);
+  }
+}
+
+// 32 bytes of row `row` at k = 64*half + 32*fg of a 128-byte-row tile.
+__device__ __forceinline__ i32x8 frag128(const uint8_t* tile, int row, int fg, int half) {
+  const int s = swz128(row), c = 4 * half + 2 * fg;
+  return join(*reinterpret_cast<const i32x4*>(tile + row * WBK + ((c ^ s) << 4)),
+              *reinterpret_cast<const i32x4*>(tile + row * WBK + (((c + 1) ^ s) << 4)));
+}
+
+// kStore: 0 = 2-byte stores, 1 = 8-byte stores (N % 4 == 0), 2 = through LDS with
+// 16-byte row stores (N % 8 == 0, output 16-byte aligned).
+template <int kStore>
+__global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
     float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
-  static_assert(kStages >= 2 && kStages <= 5, "ring depth");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
   int mt, nt;
@@ -335,47 +429,73 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_ring(
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
 
-  const int nk = (K + RBK - 1) / RBK;
+  const int nk = (K + WBK - 1) / WBK;
+  // Copies past the last step have offsets past K: the descriptor zero-fills the (free)
+  // stage without touching memory, so the loop needs no branches (a branch around the
+  // MFMAs would make the compiler copy the accumulators).
   auto issue = [&](int step) {
-    uint8_t* st = smem + (step % kStages) * kRingStageBytes;
-    dma_tile64(xa, st, rows_a, K, step * RBK, wave, lane);
-    dma_tile64(wb, st + BM * RBK, rows_b, K, step * RBK, wave, lane);
+    uint8_t* st = smem + (step & 1) * kWideStageBytes;
+    dma_tile128(xa, st, rows_a, K, step * WBK, wave, lane);
+    dma_tile128(wb, st + BM * WBK, rows_b, K, step * WBK, wave, lane);
   };
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
-    if (s < nk) issue(s);
-
   const int fr = lane % 32, fg = lane / 32;
-  constexpr int kPerStep = 2 * kRingDmaPerWave;  // DMA instructions per wave per step
-  for (int kt = 0; kt < nk; ++kt) {
-    // Step kt has landed once at most `pending` later steps' copies are outstanding.
-    const int pending = min(kStages - 2, nk - 1 - kt);
-    if (pending >= 3) wait_vmcnt<3 * kPerStep>();
-    else if (pending == 2) wait_vmcnt<2 * kPerStep>();
-    else if (pending == 1) wait_vmcnt<kPerStep>();
-    else wait_vmcnt<0>();
-    __syncthreads();  // all waves' copies of step kt landed; step kt-1's slot is free
-    if (kt + kStages - 1 < nk) issue(kt + kStages - 1);
+  const int arow = wm * WM + fr, brow = wn * WN + fr;
+  auto a_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes; };
+  auto b_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes + BM * WBK; };
 
-    const uint8_t* As = smem + (kt % kStages) * kRingStageBytes;
-    const uint8_t* Bs = As + BM * RBK;
-    i32x8 bf[4];
+  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
+  issue(0);
+  wait_vmcnt<0>();
+  __syncthreads();
+  issue(1);
+  i32x8 a0[4], b0[4], a1[4], b1[4];  // first and second half of a step
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = wn * WN + j * 32 + fr;
-      bf[j] = join(*reinterpret_cast<const i32x4*>(Bs + swizzle64(row, 2 * fg)),
-                   *reinterpret_cast<const i32x4*>(Bs + swizzle64(row, 2 * fg + 1)));
-    }
+  for (int i = 0; i < 4; ++i) {
+    b0[i] = frag128(b_tile(0), brow + 32 * i, fg, 0);
+    a0[i] = frag128(a_tile(0), arow + 32 * i, fg, 0);
+  }
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // First half: MFMAs on (a0, b0) while the second half's fragments are read.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = wm * WM + i * 32 + fr;
-      const i32x8 af = join(*reinterpret_cast<const i32x4*>(As + swizzle64(row, 2 * fg)),
-                            *reinterpret_cast<const i32x4*>(As + swizzle64(row, 2 * fg + 1)));
+      b1[i] = frag128(b_tile(kt), brow + 32 * i, fg, 1);
+      a1[i] = frag128(a_tile(kt), arow + 32 * i, fg, 1);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(bf[j], af, acc[i][j]);
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(b0[j], a0[i], acc[i][j]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
+    // Step kt+1 landed, and every wave holds step kt in registers: its stage takes
+    // step kt+2.
+    wait_vmcnt<0>();
+    __syncthreads();
+    issue(kt + 2);
+    // Second half: MFMAs on (a1, b1) while step kt+1's first-half fragments are read.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      b0[i] = frag128(b_tile(kt + 1), brow + 32 * i, fg, 0);
+      a0[i] = frag128(a_tile(kt + 1), arow + 32 * i, fg, 0);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(b1[j], a1[i], acc[i][j]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
     }
   }
-  store_transposed_block<kVec4Out>(acc, out, bias, M, N, m0, n0, wm, wn, fr, fg, rows_a, inv_scale);
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
+  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + 2 * kWideStageBytes);
+  bias_s[tid] = bias_v;
+  __syncthreads();
+  if constexpr (kStore == 2)
+    store_tile_lds(acc, out, bias_s, smem, N, m0, n0, wm, wn, fr, fg, rows_a, rows_b, inv_scale, tid);
+  else
+    store_transposed_block<kStore == 1>(acc, out, bias_s, N, m0, n0, wm, wn, fr, fg, rows_a, inv_scale);
 }
 
 // ---------------------------------------------------------------------------------------

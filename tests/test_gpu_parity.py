@@ -120,6 +120,53 @@ def test_efficient_kan_shapes(lib, shape):
         assert s["bad"] == 0, s
 
 
+# (M, K, N, output offset in bf16 elements).  K % 16 == 0 with 16-byte aligned operands
+# runs the wide kernel: its three epilogues (N % 8 == 0 and a 16-byte aligned output; N % 4
+# == 0 and 8-byte aligned; otherwise), M and N tile tails, K not a multiple of its 128-wide
+# step.  K % 16 != 0 runs the tiled kernel; M <= 64 the skinny.
+FP8_SHAPES = [
+    (300, 192, 264, 0),
+    (300, 192, 264, 4),
+    (257, 48, 260, 0),
+    (130, 16, 257, 0),
+    (333, 1000, 300, 0),
+    (65, 40, 33, 1),
+    (64, 4096, 96, 0),
+]
+
+
+@pytest.mark.parametrize("shape", FP8_SHAPES, ids=[f"M{s[0]}_K{s[1]}_N{s[2]}_off{s[3]}" for s in FP8_SHAPES])
+def test_fp8_linear_shapes(lib, shape):
+    M, K, N, off = shape
+    print(f"\n[parity] fp8_linear {shape}", flush=True)
+    inp = inputs.make_inputs("fp8_linear", dict(name="f", seed=700 + M + N, M=M, K=K, N=N))
+    args = capi.device_args("fp8_linear", inp)
+    buf = torch.full((M * N + off + 8,), float("nan"), dtype=torch.bfloat16, device="cuda")
+    out = buf[off:off + M * N].view(M, N)
+    args["output"] = out
+    want = exact.fp8_linear(inp)["output"]
+    for _ in range(2):
+        capi.call(lib, "fp8_linear", args)
+        torch.cuda.synchronize()
+        s = compare(out.cpu(), want, tasks.load_task("fp8_linear")["tolerance"])
+        assert s["bad"] == 0, s
+    assert torch.isnan(buf[:off].float()).all() and torch.isnan(buf[off + M * N:].float()).all()
+
+
+def test_fp8_linear_k0(lib):
+    """K == 0: the product is empty, so every output row is the bias (the wide kernel's
+    copies are all out of range and zero-fill)."""
+    M, N = 70, 72
+    print("\n[parity] fp8_linear K=0", flush=True)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(3)) * 0.05).to(torch.bfloat16)
+    args = dict(M=M, K=0, N=N, x_fp8=torch.empty(M, 0, dtype=torch.uint8, device="cuda"), scale_x=1.0,
+                w_fp8=torch.empty(N, 0, dtype=torch.uint8, device="cuda"), scale_w=1.0,
+                bias=bias.cuda(), output=torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda"))
+    capi.call(lib, "fp8_linear", args)
+    torch.cuda.synchronize()
+    assert torch.equal(args["output"].cpu(), bias.expand(M, N))
+
+
 @pytest.mark.parametrize("key", ["fp8_linear", "fp8_linear_m16"])
 def test_baseline_fp8_rows(lib, key):
     print(f"\n[parity] baseline {key}", flush=True)
