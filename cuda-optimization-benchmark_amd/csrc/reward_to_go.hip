@@ -11,7 +11,7 @@ namespace {
 
 constexpr int kPerLane = 8;
 constexpr int kSeg = 1;
-constexpr bool kNonTemporal = false;
+constexpr int kNonTemporal = 0;
 
 template <int kWaves>
 void launch(const float* reward, const uint8_t* done, double g, int B, int T, float* out,

@@ -11,9 +11,9 @@
 //   wave  — a log-depth suffix scan of the 64 lane maps (6 shuffle steps) gives every
 //           lane the map of the rest of its chunk of 64*kPerLane steps;
 //   workgroup — one workgroup owns one row; its kWaves waves each own kSeg consecutive
-//           chunks of a segment of kWaves*kSeg chunks, publish the composed map of their
-//           span in LDS, and each derives the value flowing into its span from the spans
-//           after it.
+//           chunks of a segment of kWaves*kSeg chunks and publishes the composed map of
+//           its span in LDS; a shuffle scan over those kWaves records gives each wave the
+//           value flowing into its span from the spans after it.
 // Segments are walked from the row end toward its start with a running carry.  Rows are
 // independent workgroups, so thousands of them stream through the CUs staggered: loads,
 // scans and stores of different rows overlap.  Maps and carries are fp64; each output is
@@ -33,7 +33,8 @@ __device__ __forceinline__ double coef(unsigned word, int byte, double g) {
 }
 }  // namespace rtg_detail
 
-template <int kWaves, int kPerLane, int kSeg, bool kVec, bool kNT>
+// kNT: bit 0 = non-temporal loads, bit 1 = non-temporal stores.
+template <int kWaves, int kPerLane, int kSeg, bool kVec, int kNT>
 __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
     const float* __restrict__ reward, const uint8_t* __restrict__ done, double g, int B, int T,
     float* __restrict__ out) {
@@ -43,13 +44,26 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
   constexpr int kQ = kPerLane / 4;
   __shared__ double span_a[kWaves], span_r[kWaves];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int nchunks = (T + kChunk - 1) / kChunk;
+
+  // gk = g^kPerLane, and pw_rest = g^(kPerLane*(63-lane)) (the A of lanes lane+1..63 with
+  // no done step), by repeated squaring.
+  double gk = 1.0;
+#pragma unroll
+  for (int e = 0; e < kPerLane; ++e) gk *= g;
+  double pw_rest = 1.0;
+  {
+    double base = gk;
+    for (int e = kWave - 1 - lane; e > 0; e >>= 1) {
+      if (e & 1) pw_rest *= base;
+      base *= base;
+    }
+  }
   const int row = blockIdx.x;
   const size_t base = (size_t)row * (size_t)T;
   const float* rr = reward + base;
   const uint8_t* dd = done + base;
   float* oo = out + base;
-  const int nchunks = (T + kChunk - 1) / kChunk;
-
   double carry = 0.0;  // value of the step after the current segment (0 past the row end)
   for (int hi = nchunks; hi > 0; hi -= kWaves * kSeg) {
     const int lo = hi > kWaves * kSeg ? hi - kWaves * kSeg : 0;
@@ -70,7 +84,7 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
         if constexpr (kVec) {
           if (t < T) {
             const f32x4* src = reinterpret_cast<const f32x4*>(rr + t);
-            const f32x4 v = kNT ? __builtin_nontemporal_load(src) : *src;
+            const f32x4 v = (kNT & 1) ? __builtin_nontemporal_load(src) : *src;
             r[c][4 * q + 0] = v.x;
             r[c][4 * q + 1] = v.y;
             r[c][4 * q + 2] = v.z;
@@ -89,32 +103,39 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
       }
     }
 
-    // Lane maps and wave suffix scans; a chunk's total map is lane 0's.  Steps past the
-    // row end hold r = 0, so they only ever multiply the zero carry of the row end.
-    double sr[kSeg], sa[kSeg];
+    // Lane maps and wave suffix scans.  A map is (R, A): v -> R + A*v.  A lane's A over its
+    // kPerLane steps is 0 if one of them is a done step, else g^kPerLane; in the suffix
+    // scan every combining lane's span is exactly kPerLane*off steps, so its A is 0 or the
+    // wave-uniform g^(kPerLane*off).  A therefore travels as one bit per lane in a 64-bit
+    // ballot mask (bit L: a done step in lanes L.. of the span), and only R is a per-lane
+    // double.  A chunk's total map is lane 0's.  Steps past the row end hold r = 0 and no
+    // done, so they only ever multiply the zero carry of the row end.
+    double sr[kSeg];
+    unsigned long long smask[kSeg];
     double wr = 0.0, wa = 1.0;  // this wave's span map
 #pragma unroll
     for (int c = kSeg - 1; c >= 0; --c) {
-      double R = 0.0, A = 1.0;
+      double R = 0.0;
 #pragma unroll
-      for (int e = kPerLane - 1; e >= 0; --e) {
-        const double a = coef(dn[c][e / 4], e % 4, g);
-        R = fma(a, R, (double)r[c][e]);
-        A = a * A;
-      }
+      for (int e = kPerLane - 1; e >= 0; --e) R = fma(coef(dn[c][e / 4], e % 4, g), R, (double)r[c][e]);
+      unsigned any = 0u;
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) any |= dn[c][q];
+      unsigned long long mask = __ballot(any != 0u);
+      double G = gk;  // g^(kPerLane*off)
 #pragma unroll
       for (int off = 1; off < kWave; off <<= 1) {
         const double Rn = __shfl_down(R, off, kWave);
-        const double An = __shfl_down(A, off, kWave);
-        if (lane + off < kWave) {
-          R = fma(A, Rn, R);
-          A = A * An;
-        }
+        const bool blocked = (mask >> lane) & 1ull;
+        if (lane + off < kWave && !blocked) R = fma(G, Rn, R);
+        mask |= mask >> off;
+        G = G * G;
       }
       sr[c] = R;
-      sa[c] = A;
+      smask[c] = mask;
       if (c0 + c < hi) {
-        const double cr = __shfl(R, 0, kWave), ca = __shfl(A, 0, kWave);
+        const double cr = __shfl(R, 0, kWave);
+        const double ca = (mask & 1ull) ? 0.0 : G;  // G is now g^(kPerLane*64)
         wr = fma(ca, wr, cr);
         wa = ca * wa;
       }
@@ -124,17 +145,36 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
       span_a[wave] = wa;
     }
     __syncthreads();
-    double cin = carry;  // value flowing into this wave's span from the later spans
-    for (int v = kWaves - 1; v > wave; --v) cin = fma(span_a[v], cin, span_r[v]);
-    double next_carry = carry;
-    for (int v = kWaves - 1; v >= 0; --v) next_carry = fma(span_a[v], next_carry, span_r[v]);
+    // Lane v holds span v; a suffix scan over the kWaves lanes composes spans v.. so that
+    // lane v holds the map from span v's start to the segment end.
+    double sa_v = lane < kWaves ? span_a[lane] : 1.0, sr_v = lane < kWaves ? span_r[lane] : 0.0;
+#pragma unroll
+    for (int off = 1; off < kWaves; off <<= 1) {
+      const double Rn = __shfl_down(sr_v, off, kWave), An = __shfl_down(sa_v, off, kWave);
+      if (lane + off < kWaves) {
+        sr_v = fma(sa_v, Rn, sr_v);
+        sa_v = sa_v * An;
+      }
+    }
+    // Value flowing into this wave's span from the later spans, and into the segment.
+    const double cin_a = __shfl(sa_v, wave + 1, kWave), cin_r = __shfl(sr_v, wave + 1, kWave);
+    double cin = wave + 1 < kWaves ? fma(cin_a, carry, cin_r) : carry;
+    const double next_carry = fma(__shfl(sa_v, 0, kWave), carry, __shfl(sr_v, 0, kWave));
 
 #pragma unroll
     for (int c = kSeg - 1; c >= 0; --c) {
       if (c0 + c >= hi) continue;
       const int t0 = (c0 + c) * kChunk + lane * kPerLane;
+      // Keep only the raw floats and done words live across the scan: without this the
+      // compiler holds the first pass's fp64 conversions and coefficients (32 VGPRs).
+#pragma unroll
+      for (int e = 0; e < kPerLane; ++e) asm volatile("" : "+v"(r[c][e]));
+#pragma unroll
+      for (int q = 0; q < kQ; ++q) asm volatile("" : "+v"(dn[c][q]));
+      // Value entering this lane's last step: lanes lane+1.. applied to cin.
       const double Rn = __shfl_down(sr[c], 1, kWave);
-      const double An = __shfl_down(sa[c], 1, kWave);
+      const bool later_done = lane + 1 < kWave && ((smask[c] >> (lane + 1)) & 1ull);
+      const double An = later_done ? 0.0 : pw_rest;
       double v = (lane == kWave - 1) ? cin : fma(An, cin, Rn);
       float o[kPerLane];
 #pragma unroll
@@ -149,7 +189,7 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
           if (t < T) {
             const f32x4 w = {o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
             f32x4* dst = reinterpret_cast<f32x4*>(oo + t);
-            if constexpr (kNT)
+            if constexpr ((kNT & 2) != 0)
               __builtin_nontemporal_store(w, dst);
             else
               *dst = w;
