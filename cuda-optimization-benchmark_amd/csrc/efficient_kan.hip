@@ -2,14 +2,15 @@
 //
 // Drop-in signature tasks/efficient_kan/tests/task.json:3, replacing
 // reference/efficient_kan/solution.cu:177-288.  Fast path (efficient_kan.hpp): spline
-// order 3 with at most 16 bases per feature — a weight-preparation launch and one fused
-// fp16x3 MFMA GEMM.  Other shapes take the row-wise fp32 path below.
+// order 3 with at most 16 knots per feature — one launch that prepares the weights and
+// basis tables, and one fused fp16x3 MFMA GEMM.  Other shapes take the row-wise fp32 path
+// below.
 #include "efficient_kan.hpp"
 
 namespace taskops {
 namespace {
 
-constexpr int kStages = 4;
+constexpr int kStages = 4;  // weight ring depth of kan_gemm
 
 // Row-wise fp32 path for shapes outside the fast path: the expanded activation row is
 // built in LDS with the Cox-de Boor recurrence, one output column per thread.
@@ -60,6 +61,16 @@ __global__ __launch_bounds__(kRowThreads) void kan_rowwise(
   if (o < O) out[(size_t)b * O + o] = acc;
 }
 
+// True when every 32-bit buffer offset of the fast path fits: x, out and the prepared
+// weights each under 2 GiB.
+bool fast_path_fits(int B, int I, int O, int Cp) {
+  using namespace kan;
+  const size_t ngroups = (I + kGroup - 1) / kGroup, Opad = ((O + BN - 1) / BN) * (size_t)BN;
+  const size_t lim = 0x7fffffffu;
+  return (size_t)B * I * 4 < lim && (size_t)B * O * 4 < lim &&
+         ngroups * (1 + Cp) * Opad * kChunk * 2 + (size_t)Opad * kChunk * 2 * kStages < lim;
+}
+
 template <int kCp>
 hipError_t launch_fast(const float* x, const float* grid, const float* wb, const float* ws,
                        const float* sc, int C, int B, int I, int O, int L, float* out,
@@ -69,25 +80,29 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const int Opad = ((O + BN - 1) / BN) * BN;
   const int nq = ngroups * (1 + kCp);
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
+  const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
   void* wsp = nullptr;
-  hipError_t e = workspace(kSlotKan, 2 * half_bytes + (size_t)Opad * sizeof(float), stream, &wsp);
+  hipError_t e = workspace(kSlotKan, 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float), stream, &wsp);
   if (e != hipSuccess) return e;
   auto* bhi = static_cast<_Float16*>(wsp);
   auto* blo = reinterpret_cast<_Float16*>(static_cast<char*>(wsp) + half_bytes);
-  auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
-  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, kCp, ngroups,
-                     Opad, bhi, blo, colscale);
+  auto* tables = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
+  auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes + table_bytes);
+  // One launch prepares the weights (Opad workgroups) and the basis tables (the rest).
+  const int table_blocks = (ngroups * kGroup + 255) / 256;
+  hipLaunchKernelGGL(kan_prepare, dim3(Opad + table_blocks), dim3(256), 0, stream, wb, ws, sc, I, O, C, kCp,
+                     ngroups, Opad, bhi, blo, colscale, grid, L, tables);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
-  const size_t lds = (size_t)kStages * kStageBytes + kKnotBytes;
+  const size_t lds = (size_t)kStages * kStageBytes + kTblBytes;
   const bool vec4 = (O % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
   if (vec4)
-    hipLaunchKernelGGL((kan_gemm<kCp, kStages, true>), dim3(tiles), dim3(kThreads), lds, stream, x, grid,
-                       B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, B, I, O, L,
+                       ngroups, Opad, bhi, blo, colscale, out);
   else
-    hipLaunchKernelGGL((kan_gemm<kCp, kStages, false>), dim3(tiles), dim3(kThreads), lds, stream, x, grid,
-                       B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, B, I, O, L,
+                       ngroups, Opad, bhi, blo, colscale, out);
   return hipGetLastError();
 }
 
@@ -107,7 +122,8 @@ extern "C" hipError_t taskops_efficient_kan(const float* x, const float* grid,
   if (B == 0 || O == 0) return hipSuccess;
   const int C = grid_size + spline_order;
   const int Cp = kan::padded_bases(C);
-  if (spline_order == kan::kOrder && I > 0 && L <= kan::kMaxKnots && (Cp == 8 || Cp == 16)) {
+  if (spline_order == kan::kOrder && I > 0 && L <= kan::kMaxKnots && (Cp == 8 || Cp == 16) &&
+      fast_path_fits(B, I, O, Cp)) {
     if (Cp == 8)
       return launch_fast<8>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
     return launch_fast<16>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
