@@ -81,28 +81,32 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const int nq = ngroups * (1 + kCp);
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
+  const int table_blocks = (ngroups * kGroup + 255) / 256;
   void* wsp = nullptr;
-  hipError_t e = workspace(kSlotKan, 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float), stream, &wsp);
+  hipError_t e = workspace(kSlotKan, 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float) +
+                                         (size_t)table_blocks * sizeof(int), stream, &wsp);
   if (e != hipSuccess) return e;
   auto* bhi = static_cast<_Float16*>(wsp);
   auto* blo = reinterpret_cast<_Float16*>(static_cast<char*>(wsp) + half_bytes);
   auto* tables = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
   auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes + table_bytes);
-  // One launch prepares the weights (Opad workgroups) and the basis tables (the rest).
-  const int table_blocks = (ngroups * kGroup + 255) / 256;
+  auto* uflags = reinterpret_cast<int*>(colscale + Opad);
+  // One launch prepares the weights (Opad workgroups) and the basis tables and their
+  // uniform-grid flags (the rest).
   hipLaunchKernelGGL(kan_prepare, dim3(Opad + table_blocks), dim3(256), 0, stream, wb, ws, sc, I, O, C, kCp,
-                     ngroups, Opad, bhi, blo, colscale, grid, L, tables);
+                     ngroups, Opad, bhi, blo, colscale, grid, L, tables, uflags);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
   const size_t lds = (size_t)kStages * kStageBytes + kTblBytes;
-  const bool vec4 = (O % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
-  if (vec4)
-    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, B, I, O, L,
-                       ngroups, Opad, bhi, blo, colscale, out);
+  const bool vec = (O % 4) == 0 && (I % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                   (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+  if (vec)
+    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, uflags,
+                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
   else
-    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, B, I, O, L,
-                       ngroups, Opad, bhi, blo, colscale, out);
+    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, uflags,
+                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
   return hipGetLastError();
 }
 

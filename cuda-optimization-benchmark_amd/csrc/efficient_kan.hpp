@@ -10,12 +10,13 @@
 // hi*hi + hi*lo + lo*hi (the dropped lo*lo term is ~2^-22 relative), accumulated in fp32.
 //
 // K order: features in groups of 32; each group is one "silu" chunk (32 features, k =
-// feature) followed by C' "spline" chunks (32/C' features x C' bases, k = feature*C' +
-// basis).  In MFMA layout lane l supplies k = 8*(l/16) .. +7 of batch row l % 16, so in
-// a spline chunk each lane owns one (row, feature) and 8 of its bases: it finds x's knot
-// interval, evaluates the four bases nonzero there from per-interval cubic coefficients
-// and shifts them into its 8 slots, straight in registers — the expanded activations
-// never touch LDS or HBM.
+// feature) followed by C' "spline" chunks; spline chunk t holds the C' bases of the 32/C'
+// features i*C' + t (k = i*C' + basis).  In MFMA layout lane l supplies k = 8*(l/16) .. +7
+// of batch row l % 16, so over one group a lane needs x at one contiguous run of C'
+// features, and in a spline chunk it owns one (row, feature) and 8 of its bases: it finds
+// x's knot interval, evaluates the four bases nonzero there from per-interval cubic
+// coefficients and shifts them into its 8 slots, straight in registers — the expanded
+// activations never touch LDS or HBM.
 //
 // Per call, kan_prepare (a) writes the weights ([Wb | Ws*sc], the A operand) in that K
 // order as fp16 hi/lo with a per-output-column power-of-two scale (so neither half under-
@@ -59,16 +60,22 @@ inline int padded_bases(int C) { return C <= 8 ? 8 : (C <= 16 ? 16 : (C <= 32 ? 
 // ---------------------------------------------------------------------------------------
 // Basis tables: for every feature, its knot row (16 floats, +inf past L) followed by, for
 // each knot interval j in [0, L-1), the cubic coefficients of the four bases j-3..j that
-// are nonzero on [t_j, t_{j+1}), as polynomials in u = x - t_j (16 floats: basis r's c0..c3
-// at [4r, 4r+4)).  A basis outside [0, C) has zero coefficients.  The polynomials come
-// from the Cox-de Boor recursion carried out on polynomials in fp64 with the reference's
-// index ranges (tasks/efficient_kan/reference.py:33-39: N_{k,p} exists for 0 <= k <=
-// L-2-p); a zero-width knot span contributes nothing.  Layout: [group][tbl_group_bytes],
-// feature fl of a group at fl * 64 * L bytes, so one group is one contiguous copy.
+// are nonzero on [t_j, t_{j+1}), as polynomials in u = x - t_j (16 floats: basis c's
+// c0..c3 in 16-byte chunk tbl_chunk(j, c % 4)).  A basis outside [0, C) has zero
+// coefficients.  The polynomials come from the Cox-de Boor recursion carried out on
+// polynomials in fp64 with the reference's index ranges (tasks/efficient_kan/
+// reference.py:33-39: N_{k,p} exists for 0 <= k <= L-2-p); a zero-width knot span
+// contributes nothing.  Layout: [group][tbl_group_bytes], feature fl of a group at
+// fl * 64 * L bytes, so one group is one contiguous copy.
 // ---------------------------------------------------------------------------------------
 constexpr int kTblBytes = 32 * 1024;  // LDS table buffer: 32 features * 64 * L bytes, L <= 16
 
 __host__ __device__ inline int tbl_group_bytes(int L) { return 4096 * ((L + 1) / 2); }
+
+// Position of basis r's 16-byte coefficient chunk within interval j's 64 bytes: XOR-ed
+// with (j >> 2) & 3, so lanes of one feature reading intervals j and j + 4 (the same banks
+// at a 64-byte stride) hit different banks.
+__host__ __device__ inline int tbl_chunk(int j, int r) { return r ^ ((j >> 2) & 3); }
 
 __host__ __device__ void kan_table_feature(const float* __restrict__ knots_row, int L, float* __restrict__ dst) {
   double t[kMaxKnots];
@@ -98,38 +105,57 @@ __host__ __device__ void kan_table_feature(const float* __restrict__ knots_row, 
       for (int r = 0; r <= kOrder; ++r)
         for (int c = 0; c < 4; ++c) P[r][c] = Q[r][c];
     }
-    for (int r = 0; r <= kOrder; ++r)
-      for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * r + c] = (float)P[r][c];
+    for (int r = 0; r <= kOrder; ++r)  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
+      for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
   }
+}
+
+// Whether a knot row is uniform enough for the GEMM's direct interval lookup: h > 0 and
+// every knot within 1e-3 h of t_0 + k h (the grids efficient-kan builds, arange * h + a
+// in fp32, are uniform to a few ulps).
+__host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, int L) {
+  if (L < 2) return false;
+  const double h = ((double)t[L - 1] - (double)t[0]) / (L - 1);
+  if (!(h > 0.0) || !(h < 1e300)) return false;
+  for (int k = 0; k < L; ++k)
+    if (!(__builtin_fabs((double)t[k] - ((double)t[0] + k * h)) <= 1e-3 * h)) return false;
+  return true;
 }
 
 // ---------------------------------------------------------------------------------------
 // Weight preparation: one workgroup per output column o.
 // bhi/blo: [nchunks][Opad][32] fp16; chunk q = g*(1+Cp) + sub; sub 0 holds Wb[o, 32g + s],
-// sub >= 1 holds (Ws*sc)[o, f, c] with f = 32g + (sub-1)*(32/Cp) + s/Cp, c = s % Cp
-// (zero past I or C).  colscale[o] = 2^-e with e chosen so max|column| * 2^e is in
-// [2^14, 2^15).
+// sub >= 1 holds (Ws*sc)[o, f, c] with f = 32g + (s/Cp)*Cp + (sub-1), c = s % Cp (zero
+// past I or C).  So over a group's spline chunks the lanes that supply slots s..s+7 of a
+// chunk walk the features (s/Cp)*Cp .. +Cp-1: the same 8 (Cp = 8) or 16 features whose
+// silu values they supply, and the GEMM loads each lane's x values as one contiguous run.
+// colscale[o] = 2^-e with e chosen so max|column| * 2^e is in [2^14, 2^15).
 // ---------------------------------------------------------------------------------------
 // Workgroups past Opad build the basis tables instead (one feature per thread), when
-// `tables` is given.
+// `tables` is given, and write uflags[block] = 1 when every knot row of the block's 256
+// features is uniform (kan_knots_uniform), else 0.
 __global__ __launch_bounds__(256) void kan_prepare(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
     int O, int C, int Cp, int ngroups, int Opad, _Float16* __restrict__ bhi,
     _Float16* __restrict__ blo, float* __restrict__ colscale, const float* __restrict__ grid = nullptr,
-    int L = 0, float* __restrict__ tables = nullptr) {
+    int L = 0, float* __restrict__ tables = nullptr, int* __restrict__ uflags = nullptr) {
   __shared__ float red[4];
   if ((int)blockIdx.x >= Opad) {
     const int f = ((int)blockIdx.x - Opad) * 256 + (int)threadIdx.x;
+    bool uniform = true;
     if (tables != nullptr && f < ngroups * kGroup) {
       float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
                                             (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
       if (f < I) {
         kan_table_feature(grid + (size_t)f * L, L, dst);
-      } else {  // missing feature: +inf knots (every basis zero) and zero coefficients
-        for (int k = 0; k < kMaxKnots; ++k) dst[k] = __builtin_inff();
+        uniform = kan_knots_uniform(grid + (size_t)f * L, L);
+      } else {  // missing feature: knots 0, 1, 2, ... and zero coefficients (every basis zero)
+        for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
         for (int k = kMaxKnots; k < 16 * L; ++k) dst[k] = 0.0f;
       }
     }
+    uniform = __syncthreads_and(uniform);
+    if (uflags != nullptr && threadIdx.x == 0) uflags[(int)blockIdx.x - Opad] = uniform ? 1 : 0;
     return;
   }
   const int o = blockIdx.x;
@@ -154,7 +180,6 @@ __global__ __launch_bounds__(256) void kan_prepare(
 
   const int per_group = 1 + Cp;
   const int total8 = ngroups * per_group * (kChunk / 8);  // 8 consecutive slots per item
-  const int feats_per_chunk = kChunk / Cp;
   for (int idx = threadIdx.x; idx < total8; idx += 256) {
     const int q = idx / (kChunk / 8), s0 = (idx % (kChunk / 8)) * 8;
     const int g = q / per_group, sub = q % per_group;
@@ -168,7 +193,7 @@ __global__ __launch_bounds__(256) void kan_prepare(
           const int f = g * kGroup + s;
           if (f < I) v = wb[(size_t)o * I + f];
         } else {
-          const int f = g * kGroup + (sub - 1) * feats_per_chunk + s / Cp;
+          const int f = g * kGroup + (s / Cp) * Cp + (sub - 1);
           const int c = s % Cp;
           if (f < I && c < C) v = ws[((size_t)o * I + f) * C + c] * sc[(size_t)o * I + f];
         }
@@ -206,34 +231,47 @@ __global__ __launch_bounds__(256) void kan_prepare(
 // weight and table copies past the end zero-fill through the buffer descriptors, so no
 // branch surrounds the MFMAs (which would make the compiler copy the accumulators).
 // ---------------------------------------------------------------------------------------
+// Weight tiles: 64-byte rows (32 fp16 of k); chunk c of row r sits at chunk c ^ ((r >> 1)
+// & 3), which spreads the 16 rows x 4 chunks of one fragment read over all banks
+// (measured on MI355X: 141 B/clk/CU against 127 unswizzled or with (r >> 2) & 3).
+__device__ __forceinline__ int swz_w(int row) { return (row >> 1) & 3; }
 __device__ __forceinline__ int swizzle64(int row, int chunk) {
-  return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
+  return row * 64 + ((chunk ^ swz_w(row)) << 4);
 }
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// Copy chunk q's hi and lo tiles (rows n0..n0+BN-1 of [q][Opad][32]) into an LDS stage.
-// A direct-to-LDS instruction writes 64 consecutive 16-byte slots (16 rows of 64 bytes);
-// lane i fetches the chunk the swizzle places in slot i.  Each wave copies
-// kGroupsPerWave groups of each half.
-__device__ __forceinline__ void dma_chunk(__amdgpu_buffer_rsrc_t rhi, __amdgpu_buffer_rsrc_t rlo,
-                                          uint8_t* stage, int q, int Opad, int n0, int wave,
-                                          int lane) {
-  const int r16 = lane / 4, logical = (lane % 4) ^ ((r16 >> 2) & 3);
+// Copy part `part` (0 .. kGroupsPerWave-1) of this wave's share of chunk q's hi and lo
+// tiles (rows n0..n0+BN-1 of [q][Opad][32]) into an LDS stage: one 16-row group of each
+// half.  A direct-to-LDS instruction writes 64 consecutive 16-byte slots (16 rows of 64
+// bytes); lane i fetches the chunk the swizzle places in slot i.
+__device__ __forceinline__ void dma_chunk_part(__amdgpu_buffer_rsrc_t rhi, __amdgpu_buffer_rsrc_t rlo,
+                                               uint8_t* stage, int q, int Opad, int n0, int wave,
+                                               int lane, int part) {
+  const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
   static_assert(kGroupsPerWave * kWaves * 16 == BN, "tile rows split evenly over waves");
-#pragma unroll
-  for (int i = 0; i < kGroupsPerWave; ++i) {
-    const int group = wave * kGroupsPerWave + i;
-    const int row = group * 16 + r16;
-    const unsigned off = (unsigned)(((size_t)q * Opad + n0 + row) * 64 + 16 * logical);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rhi, (__attribute__((address_space(3))) void*)(stage + group * 1024), 16, off, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rlo, (__attribute__((address_space(3))) void*)(stage + kTileBytes + group * 1024), 16, off,
-        0, 0, 0);
-  }
+  const int group = wave * kGroupsPerWave + part;
+  const int row = group * 16 + r16;
+  const unsigned off = (unsigned)(((size_t)q * Opad + n0 + row) * 64 + 16 * logical);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rhi, (__attribute__((address_space(3))) void*)(stage + group * 1024), 16, off, 0, 0, 0);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rlo, (__attribute__((address_space(3))) void*)(stage + kTileBytes + group * 1024), 16, off,
+      0, 0, 0);
+}
+
+// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
+// outstanding vector memory operation (vmcnt(0)), which would drain the copy ring at each
+// chunk.  Callers account for their copies with explicit vmcnt waits; LDS reads issued
+// before the barrier are complete (lgkmcnt(0)), and the signal fences keep the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_vm_drain() {
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | 0xF | (0x3 << 14));  // lgkmcnt(0) only
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 template <int n>
@@ -275,17 +313,9 @@ __device__ __forceinline__ void tile_of(int b, int tm, int tn, int& mt, int& nt)
   mt = v % tm;
 }
 
-// V (four fp16 values, low first) placed at fp16 slot p of an 8-slot window: slots p..p+3
-// of the window get V[0..3]; values outside the window are dropped.
-__device__ __forceinline__ i32x4 place4(unsigned long long V, int p) {
-  const int sh = 16 * p;
-  const unsigned long long left = V << (sh & 63), right = V >> ((-sh) & 63);
-  const unsigned long long carry = V >> ((64 - sh) & 63), left2 = V << ((sh - 64) & 63);
-  const unsigned long long lo = (sh >= 0 && sh < 64) ? left : ((sh < 0 && sh > -64) ? right : 0ull);
-  const unsigned long long hi = (sh > 0 && sh < 64) ? carry : ((sh >= 64 && sh < 128) ? left2 : 0ull);
-  return i32x4{(int)(unsigned)lo, (int)(unsigned)(lo >> 32), (int)(unsigned)hi, (int)(unsigned)(hi >> 32)};
-}
-
+// Interval lookup.  j is the knot interval (clamped to [0, L-2]) whose cubics are
+// evaluated and `inside` says whether x lies in [t_0, t_{L-1}) at all (outside, every
+// basis is zero).  The coefficient chunk m holds the basis with index = m (mod 4).
 struct TabFetch {
   f32x4 c[4];
   float tj;
@@ -293,59 +323,103 @@ struct TabFetch {
   bool inside;
 };
 
+__device__ __forceinline__ void tab_fetch(TabFetch& r, const float* fe) {
+  r.tj = fe[r.j];
+  const f32x4* cf = reinterpret_cast<const f32x4*>(fe + kMaxKnots + 16 * r.j);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) r.c[m] = cf[tbl_chunk(r.j, m)];
+}
+
 __device__ __forceinline__ void tab_knots(const float* fe, f32x4 (&kn)[4]) {
   const f32x4* k4 = reinterpret_cast<const f32x4*>(fe);
 #pragma unroll
   for (int q = 0; q < 4; ++q) kn[q] = k4[q];
 }
 
-__device__ __forceinline__ TabFetch tab_locate(float x, const f32x4 (&kn)[4], const float* fe, int L) {
+// Any knot row: j + 1 = the number of knots <= x (reference.py:36-37, x in [t_j, t_{j+1})).
+__device__ __forceinline__ TabFetch tab_locate_count(float x, const f32x4 (&kn)[4], const float* fe, int L) {
   int cnt = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) cnt += (x >= kn[q].x) + (x >= kn[q].y) + (x >= kn[q].z) + (x >= kn[q].w);
   TabFetch r;
   r.j = min(max(cnt - 1, 0), L - 2);
   r.inside = cnt >= 1 && cnt <= L - 1;
-  r.tj = fe[r.j];
-  const f32x4* cf = reinterpret_cast<const f32x4*>(fe + kMaxKnots + 16 * r.j);
-#pragma unroll
-  for (int q = 0; q < 4; ++q) r.c[q] = cf[q];
+  tab_fetch(r, fe);
   return r;
 }
 
+// Uniform knot rows (every knot within 1e-3 h of t_0 + k h): j = floor((x - t_0) / h),
+// with 1/h from the first two knots.  It can differ from the count only for x within
+// ~1e-3 h of a knot, where the cubic pieces on either side agree to (1e-3)^3 / 6 of a
+// basis value (cubic B-splines are C2 at simple knots), so the two lookups give the same
+// bases to well under the op's tolerance.
+__device__ __forceinline__ TabFetch tab_locate_uniform(float x, float t0, float inv_h, const float* fe, int L) {
+  const int j = (int)__builtin_floorf((x - t0) * inv_h);
+  TabFetch r;
+  r.j = min(max(j, 0), L - 2);
+  r.inside = j == r.j;
+  tab_fetch(r, fe);
+  return r;
+}
+
+// Evaluates the four cubics at u = x - t_j, splits them into fp16 hi/lo and routes them to
+// the lane's 8 slots (bases b0 .. b0+7).  Basis c sits in slot c - b0; the value of
+// coefficient chunk m belongs to the one basis of the window [j-3, j] with index = m
+// (mod 4), so it goes to slot m or m + 4 (b0 is a multiple of 8), or to neither when that
+// basis belongs to the other lane (Cp = 16).  With Cp = 8 (b0 = 0) bases outside [0, 8)
+// have zero coefficients, so only the routing is needed: chunk m goes to slot m + 4
+// exactly when m < j - 3.
+template <int kCp>
 __device__ __forceinline__ void tab_finish(float x, const TabFetch& t, int b0, f16x8& hi, f16x8& lo) {
   const float u = x - t.tj;
   float N[4];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const f32x4 c = t.c[r];
-    N[r] = t.inside ? fmaf(fmaf(fmaf(c.w, u, c.z), u, c.y), u, c.x) : 0.0f;
+  for (int m = 0; m < 4; ++m) {
+    const f32x4 c = t.c[m];
+    N[m] = t.inside ? fmaf(fmaf(fmaf(c.w, u, c.z), u, c.y), u, c.x) : 0.0f;
   }
   asm volatile("" : "+v"(N[0]), "+v"(N[1]), "+v"(N[2]), "+v"(N[3]));
   const f16x2 h01 = __builtin_convertvector(f32x2{N[0], N[1]}, f16x2);
   const f16x2 h23 = __builtin_convertvector(f32x2{N[2], N[3]}, f16x2);
   const f16x2 l01 = __builtin_convertvector(f32x2{N[0] - (float)h01.x, N[1] - (float)h01.y}, f16x2);
   const f16x2 l23 = __builtin_convertvector(f32x2{N[2] - (float)h23.x, N[3] - (float)h23.y}, f16x2);
-  const unsigned long long H = (unsigned long long)__builtin_bit_cast(unsigned, h01) |
-                               ((unsigned long long)__builtin_bit_cast(unsigned, h23) << 32);
-  const unsigned long long Lw = (unsigned long long)__builtin_bit_cast(unsigned, l01) |
-                                ((unsigned long long)__builtin_bit_cast(unsigned, l23) << 32);
-  const int p = t.j - kOrder - b0;
-  hi = __builtin_bit_cast(f16x8, place4(H, p));
-  lo = __builtin_bit_cast(f16x8, place4(Lw, p));
+  const unsigned H0 = __builtin_bit_cast(unsigned, h01), H1 = __builtin_bit_cast(unsigned, h23);
+  const unsigned L0 = __builtin_bit_cast(unsigned, l01), L1 = __builtin_bit_cast(unsigned, l23);
+  unsigned m0, m1, m2, m3;  // slot masks: slots 2d, 2d+1 take fp16 halves of dword d % 2
+  if constexpr (kCp == 8) {
+    const int k = min(max(t.j - kOrder, 0), 4);  // chunks m < k go to slots m + 4
+    const unsigned long long M = k < 4 ? (~0ull << (16 * k)) : 0ull;
+    m0 = (unsigned)M;
+    m1 = (unsigned)(M >> 32);
+    m2 = ~m0;
+    m3 = ~m1;
+  } else {
+    // Slot s is live iff s in [p, p+3], p = j - 3 - b0 in [-11, 11]: bit s of `act`.
+    const int p = t.j - kOrder - b0;
+    const unsigned act = (0xFu << (p + 11)) >> 11;
+    auto pair = [&](int s) {
+      return (__builtin_amdgcn_sbfe(act, s, 1) & 0xFFFFu) | (__builtin_amdgcn_sbfe(act, s + 1, 1) & 0xFFFF0000u);
+    };
+    m0 = pair(0);
+    m1 = pair(2);
+    m2 = pair(4);
+    m3 = pair(6);
+  }
+  hi = __builtin_bit_cast(f16x8, i32x4{(int)(H0 & m0), (int)(H1 & m1), (int)(H0 & m2), (int)(H1 & m3)});
+  lo = __builtin_bit_cast(f16x8, i32x4{(int)(L0 & m0), (int)(L1 & m1), (int)(L0 & m2), (int)(L1 & m3)});
 }
 
-template <int kCp, bool kVec4>
-__global__ __launch_bounds__(kThreads) void kan_gemm(
-    const float* __restrict__ x, const float* __restrict__ tables, int B, int I, int O, int L,
-    int ngroups, int Opad, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
+// kVec: O and I multiples of 4 and out, x 16-byte aligned (16-byte output stores and x
+// loads); otherwise 4-byte ones.  kUniform: every knot row passed kan_knots_uniform.
+template <int kCp, bool kVec, bool kUniform>
+__device__ __forceinline__ void kan_gemm_body(
+    uint8_t* smem, const float* __restrict__ x, const float* __restrict__ tables, int B, int I, int O,
+    int L, int ngroups, int Opad, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
     const float* __restrict__ colscale, float* __restrict__ out) {
   constexpr int kStages = 4;
   constexpr int kQ = 1 + kCp;                        // chunks per feature group
-  constexpr int kFeatsPerChunk = kChunk / kCp;
   constexpr int kPerStep = 2 * kGroupsPerWave;        // weight copy instructions per wave per chunk
-  constexpr int kX = 8 + kCp;                         // x values per lane and row block per group
-  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr int kX = kCp;                             // x values per lane and row block per group
   uint8_t* tbl = smem + kStages * kStageBytes;
   const int tm = (B + BM - 1) / BM, tn = Opad / BN;
   int mt, nt;
@@ -368,25 +442,41 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) acc[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // x values this lane needs per group and row block: slots 0..7 the silu chunk's
-  // features 8*fg..+7, slot 8+t the spline chunk t's feature.
-  auto xfeat = [&](int slot) {
-    return slot < 8 ? 8 * fg + slot : (slot - 8) * kFeatsPerChunk + (8 * fg) / kCp;
-  };
+  // This lane's features within a group are xb .. xb + kX - 1 (slot t = feature xb + t):
+  // spline chunk t expands feature xb + t, and the silu chunk's features 8*fg .. +7 are
+  // slots 8*fg - xb .. +7.
+  const int xb = ((8 * fg) / kCp) * kCp;
   float xcur[2][kX], xnext[2][kX];
   auto prefetch = [&](int g) {  // past I or B: reads as 0 (against zero weights)
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       const int row = row0 + rb * 16 + fr;
+      if constexpr (kVec) {  // I % 4 == 0: a 4-feature run is wholly inside or past I
 #pragma unroll
-      for (int t = 0; t < kX; ++t) {
-        const int f = g * kGroup + xfeat(t);
-        const unsigned off = (row < B && f < I) ? (unsigned)((row * I + f) * 4) : kOutOfRange;
-        xnext[rb][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+        for (int v = 0; v < kX / 4; ++v) {
+          const int f = g * kGroup + xb + 4 * v;
+          const unsigned off = (row < B && f < I) ? (unsigned)((row * I + f) * 4) : kOutOfRange;
+          const f32x4 val = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) xnext[rb][4 * v + e] = val[e];
+        }
+      } else {
+#pragma unroll
+        for (int t = 0; t < kX; ++t) {
+          const int f = g * kGroup + xb + t;
+          const unsigned off = (row < B && f < I) ? (unsigned)((row * I + f) * 4) : kOutOfRange;
+          xnext[rb][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+        }
       }
     }
   };
-  auto dma = [&](int q) { dma_chunk(rhi, rlo, smem + (q % kStages) * kStageBytes, q, Opad, n0, wave, lane); };
+  auto dma_part = [&](int q, int part) {
+    dma_chunk_part(rhi, rlo, smem + (q % kStages) * kStageBytes, q, Opad, n0, wave, lane, part);
+  };
+  auto dma = [&](int q) {
+#pragma unroll
+    for (int i = 0; i < kGroupsPerWave; ++i) dma_part(q, i);
+  };
   auto dma_table = [&](int g) {
     for (int i = 0; i < tper; ++i) {
       const int blk = wave * tper + i;
@@ -400,7 +490,11 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
     for (int rb = 0; rb < 2; ++rb) {
       float v[8];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = silu(xs[rb][t]);
+      for (int t = 0; t < 8; ++t) {
+        float xv = xs[rb][t];
+        if constexpr (kX > 8) xv = (fg & 1) ? xs[rb][8 + t] : xv;  // slot 8*fg - xb + t
+        v[t] = silu(xv);
+      }
       split8(v, hi[rb], lo[rb]);
     }
   };
@@ -420,12 +514,12 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
     silu_chunk(x0, ahi, alo);
   }
 
-  constexpr int kXLoads = 2 * kX;
+  constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;  // x load instructions per group
   // vmcnt counts to 63; a smaller allowance only waits for more of the later loads.
   constexpr int kW0 = kPerStep + kXLoads > 63 ? 63 : kPerStep + kXLoads;
   constexpr int kW12 = 2 * kPerStep + kXLoads > 63 ? 63 : 2 * kPerStep + kXLoads;
   for (int g = 0; g < ngroups; ++g) {
-    __syncthreads();
+    barrier_no_vm_drain();
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
@@ -440,9 +534,14 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
       if (k == 0) wait_vmcnt<kW0>();
       else if (k <= 2) wait_vmcnt<kW12>();
       else wait_vmcnt<2 * kPerStep>();
-      __syncthreads();
+      barrier_no_vm_drain();
       if (k == kQ - 1) dma_table(g + 1);
-      dma(q + kStages - 1);
+      // Chunk q+3 goes to the stage chunk q-1 used, which every wave has finished reading
+      // (barrier above).  Its copies are issued a part per quarter: issued together, the
+      // workgroup's 32 copy instructions queue at the memory pipeline and hold up the
+      // waves' MFMAs behind them.
+      static_assert(kGroupsPerWave == 4, "one copy part per quarter");
+      dma_part(q + kStages - 1, 0);
 
       const uint8_t* st = smem + (q % kStages) * kStageBytes;
       f16x8 wa[4][2], wb[4][2];
@@ -455,34 +554,46 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
         }
       };
       // 4 column blocks x 2 row blocks x 3 split terms; weights are the A operand, so a
-      // block is [o][b] (lane: batch row fr, registers: 4 consecutive columns).
+      // block is [o][b] (lane: batch row fr, registers: 4 consecutive columns).  Issued
+      // term by term over the 8 blocks, so an accumulator's next MFMA is 8 MFMAs behind
+      // its previous one (each accumulator still sums hi*hi, lo*hi, hi*lo in that order).
       auto mfma_w = [&](int j0, const f16x8 (&w)[4][2]) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
+        for (int term = 0; term < 3; ++term)
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            acc[rb][j0 + u] = mfma16(w[u][0], ahi[rb], acc[rb][j0 + u]);
-            acc[rb][j0 + u] = mfma16(w[u][1], ahi[rb], acc[rb][j0 + u]);
-            acc[rb][j0 + u] = mfma16(w[u][0], alo[rb], acc[rb][j0 + u]);
-          }
+          for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb)
+              acc[rb][j0 + u] = mfma16(term == 1 ? w[u][1] : w[u][0], term == 2 ? alo[rb] : ahi[rb], acc[rb][j0 + u]);
       };
       // The next chunk: this group's spline chunk k+1, or the next group's silu chunk.
       const bool spline_next = k + 1 < kQ;
-      const int fl = spline_next ? k * kFeatsPerChunk + (8 * fg) / kCp : 0;  // feature in group
+      const int fl = spline_next ? xb + k : 0;  // feature in group
       const float* fe = reinterpret_cast<const float*>(tbl + fl * 64 * L);
-      const int xs = spline_next ? 8 + k : 0;
+      const int xs = spline_next ? k : 0;
       f16x8 nhi[2], nlo[2];
       f32x4 kn[4];
+      f32x2 k01;
       TabFetch tf[2];
       load_w(0, wa);
-      if (spline_next) tab_knots(fe, kn);
+      if (spline_next) {
+        if constexpr (kUniform) k01 = *reinterpret_cast<const f32x2*>(fe);
+        else tab_knots(fe, kn);
+      }
       __builtin_amdgcn_sched_barrier(0);
       mfma_w(0, wa);  // Q1
       load_w(4, wb);
       __builtin_amdgcn_sched_barrier(0);
+      dma_part(q + kStages - 1, 1);
       if (spline_next) {
+        if constexpr (kUniform) {
+          const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate(xcur[rb][xs], kn, fe, L);
+          for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_uniform(xcur[rb][xs], k01.x, inv_h, fe, L);
+        } else {
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_count(xcur[rb][xs], kn, fe, L);
+        }
       }
       mfma_w(4, wb);  // Q2, interleaved with the interval count
       load_w(8, wa);
@@ -492,12 +603,14 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
         __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
       }
       __builtin_amdgcn_sched_barrier(0);
+      dma_part(q + kStages - 1, 2);
       mfma_w(8, wa);  // Q3 covers the coefficient reads
       load_w(12, wb);
       __builtin_amdgcn_sched_barrier(0);
+      dma_part(q + kStages - 1, 3);
       if (spline_next) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) tab_finish(xcur[rb][xs], tf[rb], (8 * fg) % kCp, nhi[rb], nlo[rb]);
+        for (int rb = 0; rb < 2; ++rb) tab_finish<kCp>(xcur[rb][xs], tf[rb], (8 * fg) % kCp, nhi[rb], nlo[rb]);
       } else {
         silu_chunk(xnext, nhi, nlo);
       }
@@ -527,7 +640,7 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
     for (int rb = 0; rb < 2; ++rb) {
       const int row = row0 + rb * 16 + fr;
       const f32x4 val = acc[rb][j] * cs;
-      if constexpr (kVec4) {
+      if constexpr (kVec) {
         const unsigned off = (row < B && o < O) ? (unsigned)((row * O + o) * 4) : kOutOfRange;
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val), ro, off, 0, 0);
       } else {
@@ -542,6 +655,22 @@ __global__ __launch_bounds__(kThreads) void kan_gemm(
       }
     }
   }
+}
+
+// The uniform-grid flags (one per table workgroup of kan_prepare) are read once; the branch
+// selects one of two whole loop bodies, so no branch sits inside the MFMA loop.
+template <int kCp, bool kVec>
+__global__ __launch_bounds__(kThreads) void kan_gemm(
+    const float* __restrict__ x, const float* __restrict__ tables, const int* __restrict__ uflags,
+    int nflags, int B, int I, int O, int L, int ngroups, int Opad, const _Float16* __restrict__ bhi,
+    const _Float16* __restrict__ blo, const float* __restrict__ colscale, float* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  bool ok = true;
+  for (int i = (int)threadIdx.x % kWave; i < nflags; i += kWave) ok = ok && uflags[i] != 0;
+  if (__builtin_amdgcn_ballot_w64(!ok) == 0)
+    kan_gemm_body<kCp, kVec, true>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+  else
+    kan_gemm_body<kCp, kVec, false>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
 }
 
 }  // namespace kan

@@ -88,31 +88,40 @@ def test_baseline_efficient_kan_rows(lib):
     assert s["bad"] == 0, s
 
 
-# (B, I, O, grid_size, spline_order, x_range, non-uniform knots).  Order 3 with at most 16
-# knots per feature runs the fused fp16x3 MFMA kernel (C = 4, 8, 11, 12 cover both padded
-# basis widths); the others run the row-wise fp32 kernel.  Ragged B, I and O exercise every
-# tile tail; x_range > 1 puts inputs outside the knot span.
+# (B, I, O, grid_size, spline_order, x_range, knots).  Order 3 with at most 16 knots per
+# feature runs the fused fp16x3 MFMA kernel (C = 4, 7, 8, 11, 12 cover both padded basis
+# widths); the others run the row-wise fp32 kernel.  Ragged B, I and O exercise every tile
+# tail; x_range > 1 puts inputs outside the knot span.  Knots: "uniform" (the task's grid:
+# the kernel's direct interval lookup), "random" (sorted random knots: the knot count),
+# "jitter" (uniform plus noise of 1e-4 h: still the direct lookup, which must agree with
+# the exact bases of the jittered knots).
 KAN_SHAPES = [
-    (130, 45, 70, 5, 3, 1.5, False),
-    (67, 33, 258, 9, 3, 1.0, True),
-    (40, 20, 36, 8, 3, 2.0, False),
-    (9, 30, 31, 1, 3, 1.0, False),
-    (33, 17, 19, 10, 3, 1.0, False),
-    (21, 40, 50, 6, 2, 1.2, True),
-    (16, 12, 8, 13, 1, 1.0, False),
+    (130, 45, 70, 5, 3, 1.5, "uniform"),
+    (67, 33, 258, 9, 3, 1.0, "random"),
+    (40, 20, 36, 8, 3, 2.0, "uniform"),
+    (9, 30, 31, 1, 3, 1.0, "uniform"),
+    (33, 17, 19, 10, 3, 1.0, "uniform"),
+    (50, 40, 40, 4, 3, 1.3, "random"),
+    (70, 64, 96, 5, 3, 1.2, "jitter"),
+    (21, 40, 50, 6, 2, 1.2, "random"),
+    (16, 12, 8, 13, 1, 1.0, "uniform"),
 ]
 
 
-@pytest.mark.parametrize("shape", KAN_SHAPES, ids=[f"B{s[0]}_I{s[1]}_O{s[2]}_G{s[3]}_K{s[4]}" for s in KAN_SHAPES])
+@pytest.mark.parametrize("shape", KAN_SHAPES, ids=[f"B{s[0]}_I{s[1]}_O{s[2]}_G{s[3]}_K{s[4]}_{s[6]}" for s in KAN_SHAPES])
 def test_efficient_kan_shapes(lib, shape):
-    B, I, O, G, K, xr, nonuniform = shape
+    B, I, O, G, K, xr, knots = shape
     print(f"\n[parity] efficient_kan {shape}", flush=True)
     case = dict(name="k", seed=900 + B, B=B, I=I, O=O, grid_size=G, spline_order=K, x_range=xr)
     inp = inputs.make_inputs("efficient_kan", case)
-    if nonuniform:
-        g = torch.Generator().manual_seed(B)
-        L = G + 2 * K + 1
+    g = torch.Generator().manual_seed(B)
+    L = G + 2 * K + 1
+    if knots == "random":
         inp["grid"] = torch.sort(torch.rand(I, L, generator=g) * 3.0 - 1.5, dim=1).values.contiguous()
+    elif knots == "jitter":
+        h = (inp["grid"][0, 1] - inp["grid"][0, 0]).item()
+        noise = (torch.rand(I, L, generator=g) * 2 - 1) * 1e-4 * h
+        inp["grid"] = (inp["grid"] + noise).contiguous()
     want = exact.efficient_kan(inp)["out"]
     for _ in range(2):
         got = capi.run_op(lib, "efficient_kan", inp)["out"].cpu().numpy()
