@@ -81,7 +81,7 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const int nq = ngroups * (1 + kCp);
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
-  const int table_blocks = (ngroups * kGroup + 255) / 256;
+  const int table_blocks = (ngroups * kGroup * L + 255) / 256;  // one thread per table entry
   void* wsp = nullptr;
   hipError_t e = workspace(kSlotKan, 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float) +
                                          (size_t)table_blocks * sizeof(int), stream, &wsp);
@@ -91,10 +91,13 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   auto* tables = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
   auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes + table_bytes);
   auto* uflags = reinterpret_cast<int*>(colscale + Opad);
-  // One launch prepares the weights (Opad workgroups) and the basis tables and their
-  // uniform-grid flags (the rest).
-  hipLaunchKernelGGL(kan_prepare, dim3(Opad + table_blocks), dim3(256), 0, stream, wb, ws, sc, I, O, C, kCp,
-                     ngroups, Opad, bhi, blo, colscale, grid, L, tables, uflags);
+  // One launch finds the column scales; the next packs the weights and builds the basis
+  // tables and their uniform-grid flags.
+  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, colscale);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(kan_pack<kCp>, dim3(table_blocks + (Opad / kPackCols) * ngroups), dim3(256), 0, stream, wb,
+                     ws, sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);

@@ -18,9 +18,10 @@
 // coefficients and shifts them into its 8 slots, straight in registers — the expanded
 // activations never touch LDS or HBM.
 //
-// Per call, kan_prepare (a) writes the weights ([Wb | Ws*sc], the A operand) in that K
-// order as fp16 hi/lo with a per-output-column power-of-two scale (so neither half under-
-// or overflows) and (b) tabulates each feature's knot row and per-interval basis cubics.
+// Per call, kan_prepare and kan_pack (a) write the weights ([Wb | Ws*sc], the A operand)
+// in that K order as fp16 hi/lo with a per-output-column power-of-two scale (so neither
+// half under- or overflows) and (b) tabulate each feature's knot row and per-interval
+// basis cubics.
 // The GEMM streams the weights through an LDS ring with direct-to-LDS loads, copies each
 // feature group's table into LDS, and undoes the column scale in the epilogue.
 #pragma once
@@ -77,37 +78,40 @@ __host__ __device__ inline int tbl_group_bytes(int L) { return 4096 * ((L + 1) /
 // at a 64-byte stride) hit different banks.
 __host__ __device__ inline int tbl_chunk(int j, int r) { return r ^ ((j >> 2) & 3); }
 
-__host__ __device__ void kan_table_feature(const float* __restrict__ knots_row, int L, float* __restrict__ dst) {
+// Entry j of a feature's table (dst: the feature's 16 * L floats): j = -1 writes the knot
+// row, j in [0, L-1) interval j's cubics.
+__host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, int L, int j, float* __restrict__ dst) {
+  if (j < 0) {
+    for (int k = 0; k < kMaxKnots; ++k) dst[k] = k < L ? knots_row[k] : __builtin_inff();
+    return;
+  }
   double t[kMaxKnots];
   for (int k = 0; k < kMaxKnots; ++k) t[k] = k < L ? (double)knots_row[k] : 0.0;
-  for (int k = 0; k < kMaxKnots; ++k) dst[k] = k < L ? knots_row[k] : __builtin_inff();
-  for (int j = 0; j + 1 < L; ++j) {
-    double P[kOrder + 1][4];  // P[r]: N_{j-3+r, p} as a cubic in u
-    for (int r = 0; r <= kOrder; ++r)
-      for (int c = 0; c < 4; ++c) P[r][c] = 0.0;
-    if (t[j + 1] > t[j]) P[kOrder][0] = 1.0;  // N_{j,0} on [t_j, t_{j+1})
-    for (int p = 1; p <= kOrder; ++p) {
-      double Q[kOrder + 1][4];
-      for (int r = 0; r <= kOrder; ++r) {
-        for (int c = 0; c < 4; ++c) Q[r][c] = 0.0;
-        const int k = j - kOrder + r;
-        if (r < kOrder - p || k < 0 || k > L - 2 - p) continue;
-        const double d1 = t[k + p] - t[k], d2 = t[k + p + 1] - t[k + 1];
-        if (d1 != 0.0) {  // (u + (t_j - t_k)) / d1 * N_{k,p-1}
-          const double a = (t[j] - t[k]) / d1, b = 1.0 / d1;
-          for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r][c] + (c > 0 ? b * P[r][c - 1] : 0.0);
-        }
-        if (d2 != 0.0 && r < kOrder) {  // ((t_{k+p+1} - t_j) - u) / d2 * N_{k+1,p-1}
-          const double a = (t[k + p + 1] - t[j]) / d2, b = -1.0 / d2;
-          for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r + 1][c] + (c > 0 ? b * P[r + 1][c - 1] : 0.0);
-        }
+  double P[kOrder + 1][4];  // P[r]: N_{j-3+r, p} as a cubic in u
+  for (int r = 0; r <= kOrder; ++r)
+    for (int c = 0; c < 4; ++c) P[r][c] = 0.0;
+  if (t[j + 1] > t[j]) P[kOrder][0] = 1.0;  // N_{j,0} on [t_j, t_{j+1})
+  for (int p = 1; p <= kOrder; ++p) {
+    double Q[kOrder + 1][4];
+    for (int r = 0; r <= kOrder; ++r) {
+      for (int c = 0; c < 4; ++c) Q[r][c] = 0.0;
+      const int k = j - kOrder + r;
+      if (r < kOrder - p || k < 0 || k > L - 2 - p) continue;
+      const double d1 = t[k + p] - t[k], d2 = t[k + p + 1] - t[k + 1];
+      if (d1 != 0.0) {  // (u + (t_j - t_k)) / d1 * N_{k,p-1}
+        const double a = (t[j] - t[k]) / d1, b = 1.0 / d1;
+        for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r][c] + (c > 0 ? b * P[r][c - 1] : 0.0);
       }
-      for (int r = 0; r <= kOrder; ++r)
-        for (int c = 0; c < 4; ++c) P[r][c] = Q[r][c];
+      if (d2 != 0.0 && r < kOrder) {  // ((t_{k+p+1} - t_j) - u) / d2 * N_{k+1,p-1}
+        const double a = (t[k + p + 1] - t[j]) / d2, b = -1.0 / d2;
+        for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r + 1][c] + (c > 0 ? b * P[r + 1][c - 1] : 0.0);
+      }
     }
-    for (int r = 0; r <= kOrder; ++r)  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
-      for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
+    for (int r = 0; r <= kOrder; ++r)
+      for (int c = 0; c < 4; ++c) P[r][c] = Q[r][c];
   }
+  for (int r = 0; r <= kOrder; ++r)  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
+    for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
 }
 
 // Whether a knot row is uniform enough for the GEMM's direct interval lookup: h > 0 and
@@ -123,49 +127,46 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 }
 
 // ---------------------------------------------------------------------------------------
-// Weight preparation: one workgroup per output column o.
+// Weight preparation, in two launches: kan_prepare finds each output column's scale,
+// kan_pack writes the GEMM's A operand and builds the basis tables.
 // bhi/blo: [nchunks][Opad][32] fp16; chunk q = g*(1+Cp) + sub; sub 0 holds Wb[o, 32g + s],
 // sub >= 1 holds (Ws*sc)[o, f, c] with f = 32g + (s/Cp)*Cp + (sub-1), c = s % Cp (zero
-// past I or C).  So over a group's spline chunks the lanes that supply slots s..s+7 of a
-// chunk walk the features (s/Cp)*Cp .. +Cp-1: the same 8 (Cp = 8) or 16 features whose
-// silu values they supply, and the GEMM loads each lane's x values as one contiguous run.
-// colscale[o] = 2^-e with e chosen so max|column| * 2^e is in [2^14, 2^15).
+// past I, O or C), all times 2^e.  So over a group's spline chunks the lanes that supply
+// slots s..s+7 of a chunk walk the features (s/Cp)*Cp .. +Cp-1: the same 8 (Cp = 8) or 16
+// features whose silu values they supply, and the GEMM loads each lane's x values as one
+// contiguous run.  colscale[o] = 2^-e with e chosen so max|column| * 2^e is in
+// [2^14, 2^15), so neither fp16 half under- or overflows.
 // ---------------------------------------------------------------------------------------
-// Workgroups past Opad build the basis tables instead (one feature per thread), when
-// `tables` is given, and write uflags[block] = 1 when every knot row of the block's 256
-// features is uniform (kan_knots_uniform), else 0.
+// kan_prepare: workgroup o reduces column o (contiguous rows of wb, sc and ws) to
+// colscale[o].
 __global__ __launch_bounds__(256) void kan_prepare(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
-    int O, int C, int Cp, int ngroups, int Opad, _Float16* __restrict__ bhi,
-    _Float16* __restrict__ blo, float* __restrict__ colscale, const float* __restrict__ grid = nullptr,
-    int L = 0, float* __restrict__ tables = nullptr, int* __restrict__ uflags = nullptr) {
+    int O, int C, float* __restrict__ colscale) {
   __shared__ float red[4];
-  if ((int)blockIdx.x >= Opad) {
-    const int f = ((int)blockIdx.x - Opad) * 256 + (int)threadIdx.x;
-    bool uniform = true;
-    if (tables != nullptr && f < ngroups * kGroup) {
-      float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
-                                            (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
-      if (f < I) {
-        kan_table_feature(grid + (size_t)f * L, L, dst);
-        uniform = kan_knots_uniform(grid + (size_t)f * L, L);
-      } else {  // missing feature: knots 0, 1, 2, ... and zero coefficients (every basis zero)
-        for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
-        for (int k = kMaxKnots; k < 16 * L; ++k) dst[k] = 0.0f;
-      }
-    }
-    uniform = __syncthreads_and(uniform);
-    if (uflags != nullptr && threadIdx.x == 0) uflags[(int)blockIdx.x - Opad] = uniform ? 1 : 0;
-    return;
-  }
   const int o = blockIdx.x;
-  const bool live = o < O;
   float mx = 0.0f;
-  if (live) {
-    for (int i = threadIdx.x; i < I; i += 256) {
-      mx = fmaxf(mx, fabsf(wb[(size_t)o * I + i]));
-      const float s = sc[(size_t)o * I + i];
-      for (int c = 0; c < C; ++c) mx = fmaxf(mx, fabsf(ws[((size_t)o * I + i) * C + c] * s));
+  if (o < O) {
+    // max_c |ws * s| = |s| * max_c |ws| exactly (rounding is monotonic).  Features are
+    // unrolled four at a time so each thread keeps its loads in flight together.
+    const float* wsc = ws + (size_t)o * I * C;
+    const bool vec = C % 4 == 0 && (reinterpret_cast<uintptr_t>(wsc) & 15) == 0;
+    for (int i0 = threadIdx.x; i0 < I; i0 += 4 * 256) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = i0 + u * 256;
+        if (i < I) {
+          float m = 0.0f;
+          if (vec) {
+            for (int c = 0; c < C; c += 4) {
+              const f32x4 v = *reinterpret_cast<const f32x4*>(wsc + (size_t)i * C + c);
+              m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+            }
+          } else {
+            for (int c = 0; c < C; ++c) m = fmaxf(m, fabsf(wsc[(size_t)i * C + c]));
+          }
+          mx = fmaxf(mx, fmaxf(fabsf(wb[(size_t)o * I + i]), fabsf(sc[(size_t)o * I + i]) * m));
+        }
+      }
     }
   }
   for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
@@ -175,37 +176,102 @@ __global__ __launch_bounds__(256) void kan_prepare(
   int e = 0;
   if (mx > 0.0f && mx < __builtin_inff()) e = 14 - ilogbf(mx);
   e = e > 100 ? 100 : (e < -100 ? -100 : e);
-  const float scale = ldexpf(1.0f, e);
   if (threadIdx.x == 0) colscale[o] = ldexpf(1.0f, -e);
+}
 
-  const int per_group = 1 + Cp;
-  const int total8 = ngroups * per_group * (kChunk / 8);  // 8 consecutive slots per item
-  for (int idx = threadIdx.x; idx < total8; idx += 256) {
-    const int q = idx / (kChunk / 8), s0 = (idx % (kChunk / 8)) * 8;
-    const int g = q / per_group, sub = q % per_group;
+// Basis tables, one thread per table entry (L per feature: the knot row and the L - 1
+// intervals); uflags[block] = 1 when every knot row the block wrote is uniform
+// (kan_knots_uniform), else 0.
+__device__ __forceinline__ void kan_tables_block(int block, const float* __restrict__ grid, int I, int L,
+                                                 int ngroups, float* __restrict__ tables,
+                                                 int* __restrict__ uflags) {
+  const int idx = block * 256 + (int)threadIdx.x;
+  const int f = idx / L, j = idx % L - 1;
+  bool uniform = true;
+  if (f < ngroups * kGroup) {
+    float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
+                                          (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
+    if (f < I) {
+      kan_table_entry(grid + (size_t)f * L, L, j, dst);
+      if (j < 0) uniform = kan_knots_uniform(grid + (size_t)f * L, L);
+    } else if (j < 0) {  // missing feature: knots 0, 1, 2, ... and zero coefficients
+      for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
+    } else {
+      for (int k = 0; k < 16; ++k) dst[kMaxKnots + 16 * j + k] = 0.0f;
+    }
+  }
+  uniform = __syncthreads_and(uniform);
+  if (threadIdx.x == 0) uflags[block] = uniform ? 1 : 0;
+}
+
+// kan_pack: the first tblocks workgroups build the basis tables (kan_tables_block); they
+// need nothing from the packing, so they run beside it.  Workgroup tblocks + ct + g *
+// (Opad / 8) writes the 1 + Cp chunks of feature group g for columns 8ct .. 8ct+7; thread
+// (column o, feature fl) writes all of its feature's bases, which
+// form one run of Cp slots (fl / Cp) * Cp .. in spline chunk 1 + fl % Cp, and threads
+// fl < 4 also write silu slots 8 fl .. +7.  A column's 32 threads so read its contiguous
+// ws rows, and the four threads that fill one 64-byte chunk row sit in the same wave.
+constexpr int kPackCols = 8;
+template <int kCp>
+__global__ __launch_bounds__(256) void kan_pack(
+    const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
+    int O, int C, int Opad, const float* __restrict__ colscale, _Float16* __restrict__ bhi,
+    _Float16* __restrict__ blo, const float* __restrict__ grid, int L, int ngroups, int tblocks,
+    float* __restrict__ tables, int* __restrict__ uflags) {
+  static_assert(kCp % 8 == 0 && kPackCols * kGroup == 256, "thread per (column, feature)");
+  if ((int)blockIdx.x < tblocks) {
+    kan_tables_block(blockIdx.x, grid, I, L, ngroups, tables, uflags);
+    return;
+  }
+  constexpr int kSub = 1 + kCp;
+  const int b = (int)blockIdx.x - tblocks, ntiles = Opad / kPackCols;
+  const int g = b / ntiles, oc = (int)threadIdx.x / kGroup, fl = (int)threadIdx.x % kGroup;
+  const int o = (b % ntiles) * kPackCols + oc, f = g * kGroup + fl;
+  const float scale = 1.0f / colscale[o];  // 2^e, exact
+  auto put = [&](int sub, int slot, const float* v) {
     f16x8 h8, l8;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int s = s0 + e;
-      float v = 0.0f;
-      if (live) {
-        if (sub == 0) {
-          const int f = g * kGroup + s;
-          if (f < I) v = wb[(size_t)o * I + f];
-        } else {
-          const int f = g * kGroup + (s / Cp) * Cp + (sub - 1);
-          const int c = s % Cp;
-          if (f < I && c < C) v = ws[((size_t)o * I + f) * C + c] * sc[(size_t)o * I + f];
-        }
-      }
-      v *= scale;
-      const _Float16 h = (_Float16)v;
+      const float w = v[e] * scale;
+      const _Float16 h = (_Float16)w;
       h8[e] = h;
-      l8[e] = (_Float16)(v - (float)h);
+      l8[e] = (_Float16)(w - (float)h);
     }
-    const size_t dst = ((size_t)q * Opad + o) * kChunk + s0;
+    const size_t dst = ((size_t)(g * kSub + sub) * Opad + o) * kChunk + slot;
     *reinterpret_cast<f16x8*>(bhi + dst) = h8;
     *reinterpret_cast<f16x8*>(blo + dst) = l8;
+  };
+  float v[kCp];
+#pragma unroll
+  for (int c = 0; c < kCp; ++c) v[c] = 0.0f;
+  if (o < O && f < I) {
+    const float s = sc[(size_t)o * I + f];
+    const float* row = ws + ((size_t)o * I + f) * C;
+    if (C % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
+#pragma unroll
+      for (int c4 = 0; c4 < kCp / 4; ++c4) {
+        if (4 * c4 < C) {
+          const f32x4 q = *reinterpret_cast<const f32x4*>(row + 4 * c4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[4 * c4 + e] = q[e] * s;
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kCp; ++c)
+        if (c < C) v[c] = row[c] * s;
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kCp / 8; ++h) put(1 + fl % kCp, (fl / kCp) * kCp + 8 * h, v + 8 * h);
+  if (fl < 4) {
+    float u[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int f2 = g * kGroup + 8 * fl + e;
+      u[e] = o < O && f2 < I ? wb[(size_t)o * I + f2] : 0.0f;
+    }
+    put(0, 8 * fl, u);
   }
 }
 

@@ -30,7 +30,7 @@ DOMINANT = {
     "leaky": "leaky_kernel",
     "ppo_clip": "ppo_clip_kernel",
     "efficient_kan": "kan_gemm",
-    "fp8_linear": "fp8_gemm_ring",
+    "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny",
 }
 COPY_PROBE_BYTES = 256 << 20
