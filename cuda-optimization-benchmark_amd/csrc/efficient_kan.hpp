@@ -290,9 +290,10 @@ __global__ __launch_bounds__(256) void kan_pack(
 // The activations of chunk q+1 are built during chunk q's MFMAs.  A wave issues its MFMAs
 // in order and cannot pass an outstanding wait, so each chunk runs in four quarters of 24
 // MFMAs (4 column blocks, weight fragments read a quarter ahead): the next chunk's knot
-// rows are read before Q1, whose MFMAs cover that latency; the interval count is
-// interleaved with Q2's MFMAs and then issues the coefficient reads, which Q3 covers; the
-// cubic evaluation, split and placement are interleaved with Q4's MFMAs.  The loop body is
+// rows are read before Q1, whose MFMAs cover that latency; the interval lookup is
+// interleaved with Q2's MFMAs and issues the coefficient reads, which the rest of Q2
+// covers; the cubic evaluation, split and slot routing of row block 0 are interleaved
+// with Q3's MFMAs and those of row block 1 with Q4's.  The loop body is
 // one whole feature group unrolled (every chunk kind and wait count is a constant) and
 // weight and table copies past the end zero-fill through the buffer descriptors, so no
 // branch surrounds the MFMAs (which would make the compiler copy the accumulators).
@@ -551,18 +552,27 @@ __device__ __forceinline__ void kan_gemm_body(
           (unsigned)(g * tgb + blk * 1024 + lane * 16), 0, 0, 0);
     }
   };
+  auto silu_rb = [&](const float (&xs)[2][kX], int rb, f16x8& hi, f16x8& lo) {
+    float v[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      float xv = xs[rb][t];
+      if constexpr (kX > 8) xv = (fg & 1) ? xs[rb][8 + t] : xv;  // slot 8*fg - xb + t
+      v[t] = silu(xv);
+    }
+    split8(v, hi, lo);
+  };
   auto silu_chunk = [&](const float (&xs)[2][kX], f16x8 (&hi)[2], f16x8 (&lo)[2]) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      float v[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        float xv = xs[rb][t];
-        if constexpr (kX > 8) xv = (fg & 1) ? xs[rb][8 + t] : xv;  // slot 8*fg - xb + t
-        v[t] = silu(xv);
-      }
-      split8(v, hi[rb], lo[rb]);
-    }
+    for (int rb = 0; rb < 2; ++rb) silu_rb(xs, rb, hi[rb], lo[rb]);
+  };
+  // Row block rb's activations for the next chunk (a spline chunk from this group's table,
+  // or the next group's silu chunk).
+  auto expand_rb = [&](bool spline_next, int xs, const TabFetch& tf, int rb, f16x8& hi, f16x8& lo) {
+    if (spline_next)
+      tab_finish<kCp>(xcur[rb][xs], tf, (8 * fg) % kCp, hi, lo);
+    else
+      silu_rb(xnext, rb, hi, lo);
   };
 
   // Prologue: group 0's table, weight chunks 0..2, group 0's x, its silu activations.
@@ -661,7 +671,7 @@ __device__ __forceinline__ void kan_gemm_body(
           for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_count(xcur[rb][xs], kn, fe, L);
         }
       }
-      mfma_w(4, wb);  // Q2, interleaved with the interval count
+      mfma_w(4, wb);  // Q2, interleaved with the interval lookup, which issues the coefficient reads
       load_w(8, wa);
 #pragma unroll
       for (int u = 0; u < 24; ++u) {
@@ -670,21 +680,22 @@ __device__ __forceinline__ void kan_gemm_body(
       }
       __builtin_amdgcn_sched_barrier(0);
       dma_part(q + kStages - 1, 2);
-      mfma_w(8, wa);  // Q3 covers the coefficient reads
+      expand_rb(spline_next, xs, tf[0], 0, nhi[0], nlo[0]);
+      mfma_w(8, wa);  // Q3, interleaved with row block 0's evaluation
       load_w(12, wb);
-      __builtin_amdgcn_sched_barrier(0);
-      dma_part(q + kStages - 1, 3);
-      if (spline_next) {
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) tab_finish<kCp>(xcur[rb][xs], tf[rb], (8 * fg) % kCp, nhi[rb], nlo[rb]);
-      } else {
-        silu_chunk(xnext, nhi, nlo);
-      }
-      mfma_w(12, wb);  // Q4, interleaved with the evaluation
 #pragma unroll
       for (int u = 0; u < 24; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);  // 4 VALU
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      dma_part(q + kStages - 1, 3);
+      expand_rb(spline_next, xs, tf[1], 1, nhi[1], nlo[1]);
+      mfma_w(12, wb);  // Q4, interleaved with row block 1's
+#pragma unroll
+      for (int u = 0; u < 24; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
