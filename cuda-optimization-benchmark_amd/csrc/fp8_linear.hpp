@@ -384,11 +384,13 @@ constexpr int kWideDmaPerWave = (BM * WBK / 16) / kSlotsPerInst / (kThreads / kW
 
 __device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
 
+// This wave's 8-row groups i0 .. i0+n-1 of a 256-row tile with 128-byte rows.
 __device__ __forceinline__ void dma_tile128(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows,
-                                            int K, int k0, int wave, int lane) {
+                                            int K, int k0, int wave, int lane, int i0 = 0,
+                                            int n = kWideDmaPerWave) {
   const int r8 = lane / 8, p = lane % 8;  // row within the 8-row group, physical chunk
 #pragma unroll
-  for (int i = 0; i < kWideDmaPerWave; ++i) {
+  for (int i = i0; i < i0 + n; ++i) {
     const int group = wave * kWideDmaPerWave + i;  // 8 rows per instruction
     const int row = group * 8 + r8;
     const int gk = k0 + 16 * (p ^ swz128(row));
@@ -397,6 +399,12 @@ __device__ __forceinline__ void dma_tile128(__amdgpu_buffer_rsrc_t r, uint8_t* l
         r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off,
         0, 0, 0);
   }
+}
+
+// 16 bytes (part 0 or 1) of row `row` at k = 64*half + 32*fg + 16*part of a 128-byte-row tile.
+__device__ __forceinline__ i32x4 frag128_part(const uint8_t* tile, int row, int fg, int half, int part) {
+  const int s = swz128(row), c = 4 * half + 2 * fg + part;
+  return *reinterpret_cast<const i32x4*>(tile + row * WBK + ((c ^ s) << 4));
 }
 
 // 32 bytes of row `row` at k = 64*half + 32*fg of a 128-byte-row tile.
@@ -438,6 +446,15 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     dma_tile128(xa, st, rows_a, K, step * WBK, wave, lane);
     dma_tile128(wb, st + BM * WBK, rows_b, K, step * WBK, wave, lane);
   };
+  // One of a step's 16 copy instructions per wave: copy c = 4i + j is row group 2i + j % 2
+  // of operand A (j < 2) or B.
+  auto issue_one = [&](int step, int i, int j) {
+    uint8_t* st = smem + (step & 1) * kWideStageBytes;
+    if (j < 2)
+      dma_tile128(xa, st, rows_a, K, step * WBK, wave, lane, 2 * i + (j & 1), 1);
+    else
+      dma_tile128(wb, st + BM * WBK, rows_b, K, step * WBK, wave, lane, 2 * i + (j & 1), 1);
+  };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * WM + fr, brow = wn * WN + fr;
   auto a_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes; };
@@ -473,19 +490,22 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     // step kt+2.
     wait_vmcnt<0>();
     __syncthreads();
-    issue(kt + 2);
-    // Second half: MFMAs on (a1, b1) while step kt+1's first-half fragments are read.
+    // Second half: MFMAs on (a1, b1) while step kt+1's first-half fragments are read and
+    // step kt+2's copies are issued, each MFMA with one 16-byte read and one copy (issued
+    // together, the copies queue at the memory pipeline and hold up the MFMAs behind them).
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      b0[i] = frag128(b_tile(kt + 1), brow + 32 * i, fg, 0);
-      a0[i] = frag128(a_tile(kt + 1), arow + 32 * i, fg, 0);
+      i32x4 part[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(b1[j], a1[i], acc[i][j]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = mfma32_e4m3(b1[j], a1[i], acc[i][j]);
+        issue_one(kt + 2, i, j);
+        part[j] = j < 2 ? frag128_part(b_tile(kt + 1), brow + 32 * i, fg, 0, j)
+                        : frag128_part(a_tile(kt + 1), arow + 32 * i, fg, 0, j - 2);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      b0[i] = join(part[0], part[1]);
+      a0[i] = join(part[2], part[3]);
     }
   }
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
