@@ -352,7 +352,7 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16
 
 // Bias staging for the wide kernel: thread t (kThreads == BN) loads bias[n0 + t] (zero
 // past N) before the prologue's copies, so the first copy wait covers it; the kernel then
-// writes it to LDS, where the epilogue reads it after a later barrier.
+// writes it to its LDS slot past the two stages, where the epilogue reads it.
 static_assert(kThreads == BN, "one bias value per thread");
 static_assert(BM * kTileRowBytes <= 2 * (BM + BN) * 128, "the output tile fits the two stages");
 constexpr int kBiasBytes = BN * 2;
@@ -460,9 +460,11 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
   auto a_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes; };
   auto b_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes + BM * WBK; };
 
+  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + 2 * kWideStageBytes);
   const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
   issue(0);
   wait_vmcnt<0>();
+  bias_s[tid] = bias_v;  // now, so no register holds it through the loop
   __syncthreads();
   issue(1);
   i32x8 a0[4], b0[4], a1[4], b1[4];  // first and second half of a step
@@ -509,8 +511,6 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     }
   }
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
-  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + 2 * kWideStageBytes);
-  bias_s[tid] = bias_v;
   __syncthreads();
   if constexpr (kStore == 2)
     store_tile_lds(acc, out, bias_s, smem, N, m0, n0, wm, wn, fr, fg, rows_a, rows_b, inv_scale, tid);
