@@ -115,4 +115,16 @@ hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void*
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
+// outstanding vector memory operation (vmcnt(0)), which would drain the copy ring at each
+// step.  Callers account for their copies with explicit vmcnt waits; LDS reads issued
+// before the barrier are complete (lgkmcnt(0)), and the signal fences keep the compiler
+// from moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_vm_drain() {
+  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | 0xF | (0x3 << 14));  // lgkmcnt(0) only
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 }  // namespace taskops

@@ -329,18 +329,6 @@ __device__ __forceinline__ void dma_chunk_part(__amdgpu_buffer_rsrc_t rhi, __amd
       0, 0, 0);
 }
 
-// Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
-// outstanding vector memory operation (vmcnt(0)), which would drain the copy ring at each
-// chunk.  Callers account for their copies with explicit vmcnt waits; LDS reads issued
-// before the barrier are complete (lgkmcnt(0)), and the signal fences keep the compiler
-// from moving memory accesses across it.
-__device__ __forceinline__ void barrier_no_vm_drain() {
-  __builtin_amdgcn_s_waitcnt((0x7 << 4) | (0x0 << 8) | 0xF | (0x3 << 14));  // lgkmcnt(0) only
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 template <int n>
 __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8));

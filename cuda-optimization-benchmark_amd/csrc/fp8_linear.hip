@@ -34,7 +34,7 @@ extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const 
   const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
   const size_t lds = 2 * kStageBytes;
   if (vec == 16) {
-    const size_t wide_lds = 2 * (size_t)kWideStageBytes + kBiasBytes;
+    const size_t wide_lds = kWideLdsBytes;
     const uintptr_t o = reinterpret_cast<uintptr_t>(output);
     if (N % 8 == 0 && (o & 15) == 0)
       hipLaunchKernelGGL(fp8_gemm_wide<2>, dim3(tiles), dim3(kThreads), wide_lds, stream, x_fp8, w_fp8,

@@ -312,6 +312,7 @@ __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4]
 // chunk c sits at chunk c ^ (r % 32), so both the column-wise writes and the row-wise
 // reads spread over all banks.
 constexpr int kTileRowBytes = BN * 2;  // 512
+constexpr int kCachePolicyNT = 2;       // buffer store cache-policy operand: nt
 __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16_t* out,
                                                const uint16_t* bias_s, uint8_t* tile_s, int N,
                                                int m0, int n0, int wm, int wn, int fr, int fg,
@@ -346,15 +347,17 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16
     const int r = (wave * (BM / 2 / (kThreads / kWave)) + s) * 2 + lane / 32;
     const i32x4 v = *reinterpret_cast<const i32x4*>(tile_s + r * kTileRowBytes + ((chunk ^ (r & 31)) << 4));
     const unsigned off = (r < rows_a && col_ok) ? (unsigned)(r * N + n0 + chunk * 8) * 2u : kOutOfRange;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), ob, off, 0, 0);
+    // Non-temporal (streaming) stores: the 32 MB output of a 4096^2 call otherwise sits dirty
+    // in L2 and is written back after the last workgroup ends, adding ~3 us per call.
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, v), ob, off, 0,
+                                           kCachePolicyNT);
   }
 }
 
 // Bias staging for the wide kernel: thread t (kThreads == BN) loads bias[n0 + t] (zero
-// past N) before the prologue's copies, so the first copy wait covers it; the kernel then
-// writes it to its LDS slot past the two stages, where the epilogue reads it.
+// past N); the kernel writes it to LDS past the output tile, where the epilogue reads it.
 static_assert(kThreads == BN, "one bias value per thread");
-static_assert(BM * kTileRowBytes <= 2 * (BM + BN) * 128, "the output tile fits the two stages");
+static_assert(BM * kTileRowBytes + BN * 2 <= 5 * BM * 128, "the output tile and bias fit the LDS rings");
 constexpr int kBiasBytes = BN * 2;
 __device__ __forceinline__ unsigned short load_bias(const uint16_t* bias, int n0, int rows_b, int tid) {
   const __amdgpu_buffer_rsrc_t rb = make_rsrc(bias + n0, (size_t)rows_b * 2);
@@ -368,18 +371,24 @@ __device__ __forceinline__ unsigned short load_bias(const uint16_t* bias, int n0
 // 256x256 output tile, 4 waves of 128x128 (4x4 blocks of 32x32x64 MFMAs, accumulators in
 // AGPRs), W fed as the A operand so D is the transposed block.  The copy engine's rate is
 // set by requests, not bytes: measured on MI355X, a 128-byte run per row moves ~45% more
-// per clock than a 64-byte one, and deeper buffering does not help.  So K advances in
-// steps of 128 (each tile row is one whole 128-byte line) through two 64 KiB LDS stages.
-// Each step is two halves of 64 k (16 MFMAs per wave each); the fragments of the second
-// half are read while the first half's MFMAs run, and those of the next step's first half
-// while the second half's run, so a stage is free for the next copy as soon as every wave
-// has passed the mid-step barrier.  Row r's 16-byte chunk c sits at chunk c ^ ((r >> 1) &
-// 7), which spreads any 16 consecutive rows of one chunk over all banks.  Accumulation
-// order is k ascending in 64-wide MFMA steps, as in the tiled kernel's 128-wide steps of
-// two 64-wide halves.
+// per clock than a 64-byte one.  So K advances in steps of 128 (each tile row is one whole
+// 128-byte line), each operand's 32 KiB per step through its own LDS ring: x (A) has three
+// slots, w (B) two, 160 KiB in all.  Each step is two halves of 64 k (16 MFMAs per wave
+// each); the fragments of the second half are read while the first half's MFMAs run, and
+// those of the next step's first half while the second half's run.  A copy instruction
+// moves 1 KiB and the memory pipeline takes about one per MFMA from the four waves
+// together, so issuing more at once stalls the MFMAs behind them: step kt+2's x copies go
+// out during step kt's first half, into the slot step kt-1 left (every wave passed the
+// barrier at its mid-step), and its w copies during the second half, into the slot step kt
+// left at this mid-step; one copy per two MFMAs throughout.  Row r's 16-byte chunk c sits
+// at chunk c ^ ((r >> 1) & 7), which spreads any 16 consecutive rows of one chunk over all
+// banks.  Accumulation order is k ascending in 64-wide MFMA steps, as in the tiled
+// kernel's 128-wide steps of two 64-wide halves.
 // ---------------------------------------------------------------------------------------
 constexpr int WBK = 128;
-constexpr int kWideStageBytes = (BM + BN) * WBK;                    // 64 KiB
+constexpr int kWideOperandBytes = BM * WBK;                          // 32 KiB per operand and step
+constexpr int kWideLdsBytes = 5 * kWideOperandBytes;                 // 3 x-slots + 2 w-slots: 160 KiB
+static_assert(BM == BN, "both operands' slots hold 256 rows");
 constexpr int kWideDmaPerWave = (BM * WBK / 16) / kSlotsPerInst / (kThreads / kWave);  // 8
 
 __device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
@@ -439,34 +448,22 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
 
   const int nk = (K + WBK - 1) / WBK;
   // Copies past the last step have offsets past K: the descriptor zero-fills the (free)
-  // stage without touching memory, so the loop needs no branches (a branch around the
+  // slot without touching memory, so the loop needs no branches (a branch around the
   // MFMAs would make the compiler copy the accumulators).
-  auto issue = [&](int step) {
-    uint8_t* st = smem + (step & 1) * kWideStageBytes;
-    dma_tile128(xa, st, rows_a, K, step * WBK, wave, lane);
-    dma_tile128(wb, st + BM * WBK, rows_b, K, step * WBK, wave, lane);
-  };
-  // One of a step's 16 copy instructions per wave: copy c = 4i + j is row group 2i + j % 2
-  // of operand A (j < 2) or B.
-  auto issue_one = [&](int step, int i, int j) {
-    uint8_t* st = smem + (step & 1) * kWideStageBytes;
-    if (j < 2)
-      dma_tile128(xa, st, rows_a, K, step * WBK, wave, lane, 2 * i + (j & 1), 1);
-    else
-      dma_tile128(wb, st + BM * WBK, rows_b, K, step * WBK, wave, lane, 2 * i + (j & 1), 1);
-  };
+  auto a_tile = [&](int step) { return smem + (step % 3) * kWideOperandBytes; };
+  auto b_tile = [&](int step) { return smem + (3 + (step & 1)) * kWideOperandBytes; };
+  auto copy_a = [&](int step, int g0, int n) { dma_tile128(xa, a_tile(step), rows_a, K, step * WBK, wave, lane, g0, n); };
+  auto copy_b = [&](int step, int g0, int n) { dma_tile128(wb, b_tile(step), rows_b, K, step * WBK, wave, lane, g0, n); };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * WM + fr, brow = wn * WN + fr;
-  auto a_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes; };
-  auto b_tile = [&](int step) { return smem + (step & 1) * kWideStageBytes + BM * WBK; };
 
-  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + 2 * kWideStageBytes);
-  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
-  issue(0);
-  wait_vmcnt<0>();
-  bias_s[tid] = bias_v;  // now, so no register holds it through the loop
+  // Prologue: steps 0 and 1 (x then w each), then step 0's first-half fragments.
+  copy_a(0, 0, kWideDmaPerWave);
+  copy_b(0, 0, kWideDmaPerWave);
+  copy_a(1, 0, kWideDmaPerWave);
+  copy_b(1, 0, kWideDmaPerWave);
+  wait_vmcnt<2 * kWideDmaPerWave>();
   __syncthreads();
-  issue(1);
   i32x8 a0[4], b0[4], a1[4], b1[4];  // first and second half of a step
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -475,33 +472,35 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
   }
 
   for (int kt = 0; kt < nk; ++kt) {
-    // First half: MFMAs on (a0, b0) while the second half's fragments are read.
+    // First half: MFMAs on (a0, b0) while the second half's fragments are read and step
+    // kt+2's x copies go out, each MFMA with one 16-byte read and every other one a copy.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      b1[i] = frag128(b_tile(kt), brow + 32 * i, fg, 1);
-      a1[i] = frag128(a_tile(kt), arow + 32 * i, fg, 1);
+      i32x4 part[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma32_e4m3(b0[j], a0[i], acc[i][j]);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      for (int j = 0; j < 4; ++j) {
+        acc[i][j] = mfma32_e4m3(b0[j], a0[i], acc[i][j]);
+        if (j % 2 == 0) copy_a(kt + 2, 2 * i + j / 2, 1);
+        part[j] = j < 2 ? frag128_part(b_tile(kt), brow + 32 * i, fg, 1, j)
+                        : frag128_part(a_tile(kt), arow + 32 * i, fg, 1, j - 2);
+        __builtin_amdgcn_sched_barrier(0);
       }
+      b1[i] = join(part[0], part[1]);
+      a1[i] = join(part[2], part[3]);
     }
-    // Step kt+1 landed, and every wave holds step kt in registers: its stage takes
-    // step kt+2.
-    wait_vmcnt<0>();
-    __syncthreads();
+    // Step kt+1 landed (only step kt+2's x copies, issued since, may be outstanding), and
+    // every wave holds step kt in registers.
+    wait_vmcnt<kWideDmaPerWave>();
+    barrier_no_vm_drain();
     // Second half: MFMAs on (a1, b1) while step kt+1's first-half fragments are read and
-    // step kt+2's copies are issued, each MFMA with one 16-byte read and one copy (issued
-    // together, the copies queue at the memory pipeline and hold up the MFMAs behind them).
+    // step kt+2's w copies go out into the slot step kt just left.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       i32x4 part[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[i][j] = mfma32_e4m3(b1[j], a1[i], acc[i][j]);
-        issue_one(kt + 2, i, j);
+        if (j % 2 == 0) copy_b(kt + 2, 2 * i + j / 2, 1);
         part[j] = j < 2 ? frag128_part(b_tile(kt + 1), brow + 32 * i, fg, 0, j)
                         : frag128_part(a_tile(kt + 1), arow + 32 * i, fg, 0, j - 2);
         __builtin_amdgcn_sched_barrier(0);
@@ -510,12 +509,23 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
       a0[i] = join(part[2], part[3]);
     }
   }
+  // The bias (L2-resident) is loaded only now: no LDS is free during the loop and a
+  // register held through it would spill.
+  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
+  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + BM * kTileRowBytes);
+  bias_s[tid] = bias_v;
   __syncthreads();
+  // The epilogue's thread indices come from an opaque copy of tid, so the compiler cannot
+  // compute them before the loop and carry them through it (where no register is free).
+  int et = tid;
+  asm volatile("" : "+v"(et));
+  const int ew = et / kWave, el = et % kWave;
+  const int ewm = ew / kWavesN, ewn = ew % kWavesN, efr = el % 32, efg = el / 32;
   if constexpr (kStore == 2)
-    store_tile_lds(acc, out, bias_s, smem, N, m0, n0, wm, wn, fr, fg, rows_a, rows_b, inv_scale, tid);
+    store_tile_lds(acc, out, bias_s, smem, N, m0, n0, ewm, ewn, efr, efg, rows_a, rows_b, inv_scale, et);
   else
-    store_transposed_block<kStore == 1>(acc, out, bias_s, N, m0, n0, wm, wn, fr, fg, rows_a, inv_scale);
+    store_transposed_block<kStore == 1>(acc, out, bias_s, N, m0, n0, ewm, ewn, efr, efg, rows_a, inv_scale);
 }
 
 // ---------------------------------------------------------------------------------------
