@@ -220,116 +220,4 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
   }
 }
 
-// Persistent variant for rows of at most one segment (T <= kWaves * 64 * kPerLane): the
-// grid's workgroups walk rows blockIdx.x, + gridDim.x, ..., and each loads its next row
-// before it scans and stores the current one, so a workgroup keeps a row of loads in flight
-// while it works (the wait for row n+1's loads at the next iteration leaves row n's
-// stores, issued after them, outstanding).  Same maps, scans and rounding as above.
-template <int kWaves, int kPerLane>
-__global__ __launch_bounds__(kWaves * 64) void reward_to_go_rows(
-    const float* __restrict__ reward, const uint8_t* __restrict__ done, double g, int B, int T,
-    float* __restrict__ out) {
-  using namespace rtg_detail;
-  static_assert(kPerLane % 4 == 0, "lanes own whole 16-byte reward vectors");
-  constexpr int kChunk = kWave * kPerLane;
-  constexpr int kQ = kPerLane / 4;
-  __shared__ double span_a[2][kWaves], span_r[2][kWaves];
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  double gk = 1.0;
-#pragma unroll
-  for (int e = 0; e < kPerLane; ++e) gk *= g;
-  double pw_rest = 1.0;
-  {
-    double base = gk;
-    for (int e = kWave - 1 - lane; e > 0; e >>= 1) {
-      if (e & 1) pw_rest *= base;
-      base *= base;
-    }
-  }
-  const int t0 = wave * kChunk + lane * kPerLane;  // this lane's first step in the row
-  float r[kPerLane];
-  unsigned dn[kQ];
-  auto load = [&](int row) {
-    const float* rr = reward + (size_t)row * T;
-    const uint8_t* dd = done + (size_t)row * T;
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int t = t0 + 4 * q;
-      f32x4 v = {0.f, 0.f, 0.f, 0.f};
-      unsigned d = 0u;
-      if (row < B && t < T) {
-        v = *reinterpret_cast<const f32x4*>(rr + t);
-        d = *reinterpret_cast<const unsigned*>(dd + t);
-      }
-      r[4 * q + 0] = v.x;
-      r[4 * q + 1] = v.y;
-      r[4 * q + 2] = v.z;
-      r[4 * q + 3] = v.w;
-      dn[q] = d;
-    }
-  };
-  int row = blockIdx.x;
-  load(row);
-  for (int it = 0; row < B; ++it, row += gridDim.x) {
-    float rc[kPerLane];
-    unsigned dc[kQ];
-#pragma unroll
-    for (int e = 0; e < kPerLane; ++e) rc[e] = r[e];
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) dc[q] = dn[q];
-    load(row + gridDim.x);  // in flight through this row's scan and stores
-
-    double R = 0.0;
-#pragma unroll
-    for (int e = kPerLane - 1; e >= 0; --e) R = fma(coef(dc[e / 4], e % 4, g), R, (double)rc[e]);
-    unsigned any = 0u;
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) any |= dc[q];
-    unsigned long long mask = __ballot(any != 0u);
-    double G = gk;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const double Rn = __shfl_down(R, off, kWave);
-      const bool blocked = (mask >> lane) & 1ull;
-      if (lane + off < kWave && !blocked) R = fma(G, Rn, R);
-      mask |= mask >> off;
-      G = G * G;
-    }
-    const int buf = it & 1;  // span records alternate, so one barrier per row suffices
-    if (lane == 0) {
-      span_r[buf][wave] = R;
-      span_a[buf][wave] = (mask & 1ull) ? 0.0 : G;
-    }
-    __syncthreads();
-    double sa_v = lane < kWaves ? span_a[buf][lane] : 1.0, sr_v = lane < kWaves ? span_r[buf][lane] : 0.0;
-#pragma unroll
-    for (int off = 1; off < kWaves; off <<= 1) {
-      const double Rn = __shfl_down(sr_v, off, kWave), An = __shfl_down(sa_v, off, kWave);
-      if (lane + off < kWaves) {
-        sr_v = fma(sa_v, Rn, sr_v);
-        sa_v = sa_v * An;
-      }
-    }
-    // Value flowing into this wave's span: the later spans applied to the row end's 0.
-    const double cin_r = __shfl(sr_v, wave + 1, kWave);
-    const double cin = wave + 1 < kWaves ? cin_r : 0.0;
-    const double Rn = __shfl_down(R, 1, kWave);
-    const bool later_done = lane + 1 < kWave && ((mask >> (lane + 1)) & 1ull);
-    const double An = later_done ? 0.0 : pw_rest;
-    double v = (lane == kWave - 1) ? cin : fma(An, cin, Rn);
-    float o[kPerLane];
-#pragma unroll
-    for (int e = kPerLane - 1; e >= 0; --e) {
-      v = fma(coef(dc[e / 4], e % 4, g), v, (double)rc[e]);
-      o[e] = (float)v;
-    }
-    float* oo = out + (size_t)row * T;
-#pragma unroll
-    for (int q = 0; q < kQ; ++q) {
-      const int t = t0 + 4 * q;
-      if (t < T) *reinterpret_cast<f32x4*>(oo + t) = f32x4{o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]};
-    }
-  }
-}
-
 }  // namespace taskops
