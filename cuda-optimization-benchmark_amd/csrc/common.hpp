@@ -107,9 +107,10 @@ enum WorkspaceSlot : int {
 };
 
 // Returns a zero-initialised device buffer of at least `bytes` for `slot` on the current
-// device, allocated on the first request and kept until the process exits.  The zero
-// fill is enqueued on `stream`, so it is ordered before the caller's first launch.
-// A later request for more bytes than the first one returns hipErrorInvalidValue.
+// device, allocated on the first request.  A later request for more bytes allocates a
+// larger one (the old one is kept until the process exits, since kernels enqueued before
+// may still use it).  The zero fill is a kernel enqueued on `stream`, ordered before the
+// caller's launches.
 hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void** out);
 
 // Number of compute units of the current device (cached per device).

@@ -21,6 +21,13 @@ Region g_regions[kMaxDevices][kNumSlots];
 std::vector<void*> g_retired;
 int g_cus[kMaxDevices] = {0};
 
+// Zero fill as a kernel rather than hipMemsetAsync: no library call enqueues memset work,
+// which keeps memset nodes out of any graph a caller captures.
+__global__ void zero_fill(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (size_t)gridDim.x * blockDim.x)
+    p[i] = uint4{0u, 0u, 0u, 0u};
+}
+
 }  // namespace
 
 hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void** out) {
@@ -31,11 +38,14 @@ hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void*
   std::lock_guard<std::mutex> lock(g_mu);
   Region& r = g_regions[dev][slot];
   if (r.bytes < bytes) {
-    size_t want = bytes < 4096 ? 4096 : bytes;
+    const size_t want = ((bytes < 4096 ? 4096 : bytes) + 15) / 16 * 16;
     void* p = nullptr;
     e = hipMalloc(&p, want);
     if (e != hipSuccess) return e;
-    e = hipMemsetAsync(p, 0, want, stream);
+    const size_t n16 = want / 16;
+    const unsigned blocks = (unsigned)(n16 / 256 < 4096 ? (n16 + 255) / 256 : 4096);
+    hipLaunchKernelGGL(zero_fill, dim3(blocks), dim3(256), 0, stream, static_cast<uint4*>(p), n16);
+    e = hipGetLastError();
     if (e != hipSuccess) {
       (void)hipFree(p);
       return e;
