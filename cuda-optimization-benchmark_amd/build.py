@@ -50,6 +50,7 @@ KERNEL_SOURCES = [
     "leaky.hip",
     "efficient_kan.hip",
     "fp8_linear.hip",
+    "quantize_e4m3.hip",
 ]
 
 OPS = ["pow_abs_sqrt_mean", "leaky", "reward_to_go", "ppo_clip", "efficient_kan", "fp8_linear"]

@@ -48,6 +48,9 @@ ENTRY = {
     "fp8_linear": ("taskops_fp8_linear",
                    [("M", _I32), ("K", _I32), ("N", _I32), ("x_fp8", _P), ("scale_x", _F32),
                     ("w_fp8", _P), ("scale_w", _F32), ("bias", _P), ("output", _P)]),
+    # Not a task op: the quantisation step before fp8_linear (reference.py:15-18).
+    "quantize_e4m3": ("taskops_quantize_e4m3",
+                      [("x", _P), ("n", _I64), ("q", _P), ("scale", _P)]),
 }
 
 EXPORTS = ["taskops_version"] + [v[0] for v in ENTRY.values()]

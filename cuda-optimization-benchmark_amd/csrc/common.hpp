@@ -103,7 +103,8 @@ enum WorkspaceSlot : int {
   kSlotPpo = 1,
   kSlotKan = 2,
   kSlotFp8 = 3,
-  kNumSlots = 4,
+  kSlotQuant = 4,
+  kNumSlots = 5,
 };
 
 // Returns a zero-initialised device buffer of at least `bytes` for `slot` on the current

@@ -105,6 +105,17 @@ hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_
                               float scale_x, const uint8_t* w_fp8, float scale_w,
                               const uint16_t* bias, uint16_t* output, hipStream_t stream);
 
+/* Per-tensor max-abs OCP e4m3 quantisation of x[n] (fp32), the step that produces
+ * fp8_linear's operands: *scale = fp32(448 / max(max|x|, 1e-9)) with the quotient in fp64,
+ * q[i] = e4m3(clamp(x[i] * *scale, -448, 448)), round to nearest even; a NaN in x makes
+ * *scale and every q[i] NaN (0x7F or 0xFF: the sign of a computed NaN is unspecified).
+ * q and scale are device pointers.  n == 0 writes nothing;
+ * n < 0 returns hipErrorInvalidValue.
+ * Replaces: tasks/fp8_linear/reference.py:15-18 (`_quantize`, which the reference runs on
+ *           the CPU before the op). */
+hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* q, float* scale,
+                                 hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,147 @@
+"""Per-tensor e4m3 quantisation (tasks/fp8_linear/reference.py:15-18): the oracle, pinned,
+and the HIP path (taskops_quantize_e4m3) against it, bit for bit.
+
+The oracle's encode() is pinned against torch's float8_e4m3fn cast on every e4m3 value,
+every midpoint between neighbours and the fp32 values either side of it, signed zeros,
+signed NaN and random values; quantize() is pinned against cob_amd.inputs.quantize_e4m3,
+whose output the golden input digests pin to the reference's own `_quantize`.  Bytes
+must match exactly except NaN results, where 0x7F and 0xFF both count (e4m3.same_codes).
+"""
+import numpy as np
+import pytest
+import torch
+
+from cob_amd import capi, inputs
+from oracle import e4m3
+
+
+def _special_values() -> np.ndarray:
+    pos = e4m3.TABLE[:0x7F]
+    vals = []
+    for i in range(len(pos)):
+        vals.append(pos[i])
+        if i + 1 < len(pos):
+            mid = np.float32((pos[i] + pos[i + 1]) / 2)
+            vals += [mid, np.nextafter(mid, np.float32(0)), np.nextafter(mid, np.float32(1000))]
+    v = np.array(vals, dtype=np.float32)
+    return np.concatenate([v, -v, np.array([0.0, -0.0, 1e-30, -1e-30, 448.0, -448.0], np.float32)])
+
+
+def test_encode_matches_torch_cast():
+    rng = np.random.default_rng(0)
+    v = np.concatenate([_special_values(), np.array([np.nan, -np.nan], np.float32),
+                        rng.uniform(-448, 448, 100_000).astype(np.float32),
+                        (rng.standard_normal(100_000) * 0.01).astype(np.float32)])
+    want = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(e4m3.encode(v), want)
+
+
+def test_encode_decode_round_trip():
+    codes = np.array([c for c in range(256) if (c & 0x7F) != 0x7F], dtype=np.uint8)
+    assert np.array_equal(e4m3.encode(e4m3.decode(codes)), codes)
+
+
+@pytest.mark.parametrize("kind", ["normal", "wide", "zeros", "one", "nan", "inf", "tiny"])
+def test_quantize_matches_pinned_inputs(kind):
+    g = torch.Generator().manual_seed(11)
+    x = {"normal": torch.randn(3001, generator=g),
+         "wide": torch.randn(517, generator=g) * 1e4,
+         "zeros": torch.zeros(64),
+         "one": torch.tensor([-2.5]),
+         "nan": torch.randn(100, generator=g).index_fill_(0, torch.tensor([37]), float("nan")),
+         "inf": torch.randn(100, generator=g).index_fill_(0, torch.tensor([5]), float("inf")),
+         "tiny": torch.randn(100, generator=g) * 1e-20}[kind]
+    q_want, s_want = inputs.quantize_e4m3(x)
+    q, s = e4m3.quantize(x.numpy())
+    assert e4m3.same_codes(q, q_want.view(torch.uint8).numpy())
+    assert (np.isnan(s) and np.isnan(s_want)) or np.float32(s) == np.float32(s_want)
+
+
+def test_quantize_closed_forms():
+    x = np.array([1.0, -3.0, 0.5], np.float32)
+    q, s = e4m3.quantize(x)
+    assert s == np.float32(448.0 / 3.0)
+    assert q[1] == 0xFE                      # -amax maps to -448
+    assert e4m3.decode(q)[0] == pytest.approx(448.0 / 3.0, rel=2 ** -3)
+
+
+# -------------------------------------------------------------------------------------
+# HIP path
+# -------------------------------------------------------------------------------------
+
+def _run_gpu(lib, x: torch.Tensor, q_off: int = 0, x_off: int = 0):
+    n = x.numel()
+    xb = torch.empty(n + x_off, dtype=torch.float32, device="cuda")
+    xd = xb[x_off:]
+    xd.copy_(x.reshape(-1))
+    qb = torch.full((n + q_off + 64,), 0xA5, dtype=torch.uint8, device="cuda")
+    qd = qb[q_off:q_off + n]
+    sd = torch.full((1,), -7.0, device="cuda")
+    capi.call(lib, "quantize_e4m3", dict(x=xd, n=n, q=qd, scale=sd))
+    torch.cuda.synchronize()
+    tail = qb[q_off + n:].cpu()
+    assert (tail == 0xA5).all() and (qb[:q_off].cpu() == 0xA5).all(), "write outside q"
+    return qd.cpu().numpy(), np.float32(sd.item())
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 65537, 1 << 20])
+def test_gpu_quantize_sizes(lib, n):
+    print(f"\n[parity] quantize_e4m3 n={n}", flush=True)
+    x = torch.randn(n, generator=torch.Generator().manual_seed(n)) * 3.0
+    q, s = _run_gpu(lib, x)
+    q_want, s_want = e4m3.quantize(x.numpy())
+    assert s == s_want
+    assert np.array_equal(q, q_want)
+
+
+@pytest.mark.gpu
+def test_gpu_quantize_cast_table(lib):
+    """Every e4m3 value, midpoint and neighbour with scale exactly 1 (|x| max = 448): the
+    hardware conversion's rounding, signed zeros and subnormals."""
+    x = torch.from_numpy(_special_values())
+    q, s = _run_gpu(lib, x)
+    assert s == np.float32(1.0)
+    assert np.array_equal(q, e4m3.encode(x.numpy()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("case", ["nan", "zeros", "inf", "unaligned"])
+def test_gpu_quantize_edges(lib, case):
+    print(f"\n[parity] quantize_e4m3 {case}", flush=True)
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(10_003, generator=g)
+    q_off = x_off = 0
+    if case == "nan":
+        x[4321] = float("nan")
+    elif case == "zeros":
+        x = torch.zeros(4099)
+    elif case == "inf":
+        x[17] = float("-inf")
+    else:
+        q_off, x_off = 3, 1
+    q, s = _run_gpu(lib, x, q_off=q_off, x_off=x_off)
+    q_want, s_want = e4m3.quantize(x.numpy())
+    assert (np.isnan(s) and np.isnan(s_want)) or s == s_want
+    assert e4m3.same_codes(q, q_want)
+
+
+@pytest.mark.gpu
+def test_gpu_quantize_baseline_operands(lib):
+    """The fp8_linear BASELINE operands: quantising the bf16-rounded x on the GPU gives the
+    bytes and scale the input builder makes on the CPU."""
+    g = torch.Generator().manual_seed(404)
+    x = torch.randn(4096, 4096, generator=g).to(torch.bfloat16).float()
+    q, s = _run_gpu(lib, x)
+    q_want, s_want = inputs.quantize_e4m3(x)
+    assert s == np.float32(s_want)
+    assert np.array_equal(q, q_want.view(torch.uint8).numpy().reshape(-1))
+
+
+@pytest.mark.gpu
+def test_gpu_quantize_empty_writes_nothing(lib):
+    sd = torch.full((1,), -7.0, device="cuda")
+    capi.call(lib, "quantize_e4m3", dict(x=torch.empty(0, device="cuda"), n=0,
+                                         q=torch.empty(0, dtype=torch.uint8, device="cuda"), scale=sd))
+    torch.cuda.synchronize()
+    assert sd.item() == -7.0
