@@ -56,9 +56,13 @@ WORKLOADS = {
                    "fp8_linear M=4096 K=N=4096 e4m3 -> bf16"),
     "fp8_linear_m16": ("fp8_linear", "fp8_linear_m16", "hbm", 16_982_016, "fp8",
                        "fp8_linear M=16 K=N=4096 e4m3 -> bf16 (weight stream)"),
+    # Not a task op: the per-tensor quantiser that makes fp8_linear's operands, run over the
+    # BASELINE x (4096x4096 bf16-rounded N(0,1), fp32).  4 bytes in + 1 out per element.
+    "quantize_e4m3": ("quantize_e4m3", "fp8_linear", "hbm", 5 * 4096 * 4096, "f32",
+                      "quantize_e4m3 x fp32 [4096,4096] -> e4m3 + fp32 scale (fp8_linear operand)"),
 }
 ORDER = ["reward_to_go", "pow_abs_sqrt_mean", "leaky", "ppo_clip", "efficient_kan", "fp8_linear",
-         "fp8_linear_m16"]
+         "fp8_linear_m16", "quantize_e4m3"]
 
 
 def _log(msg: str) -> None:
@@ -70,9 +74,20 @@ def _copies(nbytes: int) -> int:
     return max(1, min(24, -(-2 * MALL_BYTES // max(nbytes, 1))))
 
 
+def _quant_inputs(case):
+    """The fp32 x that fp8_linear's BASELINE input builder quantises (same generator)."""
+    import torch
+    g = torch.Generator().manual_seed(case.get("seed", 0))
+    return {"x": torch.randn(case["M"], case["K"], generator=g).to(torch.bfloat16).float()}
+
+
 def _device_sets(op, inp, n):
     import torch
     from cob_amd import capi
+    if op == "quantize_e4m3":
+        x = inp["x"].reshape(-1)
+        return [dict(x=x.to("cuda"), n=x.numel(), q=torch.empty(x.numel(), dtype=torch.uint8, device="cuda"),
+                     scale=torch.empty(1, device="cuda")) for _ in range(n)]
     sets = []
     shapes = None if op == "ppo_clip" else capi.output_shapes(op, inp)
     for _ in range(n):
@@ -188,7 +203,7 @@ def main() -> int:
         entry, bkey, bound, work, dtype, desc = WORKLOADS[key]
         case = tasks.BASELINE[bkey]
         _log(f"[bench] {key}: generating inputs")
-        inp = inputs.make_inputs(entry, case)
+        inp = _quant_inputs(case) if entry == "quantize_e4m3" else inputs.make_inputs(entry, case)
         probe = _device_sets(entry, inp, 1)
         per_set = _set_bytes(probe[0])
         n = _copies(per_set) if bound == "hbm" else 1

@@ -7,22 +7,35 @@
 // A NaN in x makes amax, scale and every q NaN: torch's max, Python's max(nan, 1e-9) and
 // the casts all keep it.
 //
-// Two launches over x (HBM-bound).  qz_amax reduces |x| per workgroup as raw bits: for
-// |x| the IEEE order is the unsigned-integer order and every NaN sorts above inf, so an
-// integer max propagates NaN; each workgroup writes one partial.  qz_cast reduces those
-// partials (every workgroup, a few KiB from L2), derives the scale, and converts 16
-// values per thread with v_cvt_pk_fp8_f32 into one 16-byte store.  Algorithmic bytes are
-// 4 in + 1 out per element; the second read of x is the price of the global max.
+// Two launches over x (HBM-bound; algorithmic bytes are 4 in + 1 out per element, the
+// second read of x is the price of the global max).  qz_amax reduces |x| per workgroup
+// as raw bits: for |x| the IEEE order is the unsigned-integer order and every NaN sorts
+// above inf, so an integer max propagates NaN; each workgroup writes one partial.
+// qz_cast reduces those partials (a few KiB from L2), derives the scale and converts
+// with v_cvt_pk_fp8_f32.
+//
+// Both kernels walk x in chunks of 16384 elements per workgroup and step.  A thread
+// issues all 16 of its 16-byte loads of a chunk before it uses any (64 floats in
+// registers), so each wave keeps 16 KiB in flight: at one chunk per workgroup, which a
+// 4096 x 4096 operand is on 256 CUs, a kernel is one round trip of loads.  Element
+// base + 4 * (k * 256 + t) + c of a chunk belongs to thread t, so every load and store
+// instruction of a wave covers contiguous memory.
+//
+// A single launch that keeps x in registers across a grid barrier would read x once,
+// but its barrier needs every workgroup resident: a cooperative launch guarantees that
+// and costs about 100 us per launch on this stack (measured), and a plain launch does
+// not guarantee it.
 #include "common.hpp"
 
 namespace taskops {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kPerThread = 16;  // elements per thread per grid-stride step
+constexpr int kVecs = 16;                                       // f32x4 per thread per chunk
+constexpr int64_t kChunk = (int64_t)kThreads * kVecs * 4;        // elements per chunk
+constexpr int kPerThread = 16;  // elements per thread per step of the unaligned kernels
 constexpr int kMaxPartials = 2048;
 using f32x4 = float __attribute__((ext_vector_type(4)));
-using u32x4 = unsigned __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ unsigned abs_bits(float v) { return __float_as_uint(v) & 0x7FFFFFFFu; }
 
@@ -44,27 +57,34 @@ __device__ __forceinline__ unsigned block_max_u32(unsigned v, unsigned* lds) {
   return m;
 }
 
-template <bool kVec>
-__global__ __launch_bounds__(kThreads) void qz_amax(const float* __restrict__ x, int64_t n,
-                                                    unsigned* __restrict__ partial) {
-  __shared__ unsigned lds[kThreads / kWave];
-  unsigned m = 0u;
-  const int64_t stride = (int64_t)gridDim.x * kThreads * kPerThread;
-  for (int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * kPerThread; i0 < n; i0 += stride) {
-    if (kVec && i0 + kPerThread <= n) {
-      const f32x4* p = reinterpret_cast<const f32x4*>(x + i0);
-      f32x4 v[kPerThread / 4];
+// This thread's 64 elements of the chunk at `base` (x 16-byte aligned); elements at or
+// beyond n read as 0, which never raises the max.
+__device__ __forceinline__ void load_chunk(const float* __restrict__ x, int64_t n, int64_t base, f32x4 (&v)[kVecs]) {
+  if (base + kChunk <= n) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(x + base) + threadIdx.x;
 #pragma unroll
-      for (int k = 0; k < kPerThread / 4; ++k) v[k] = __builtin_nontemporal_load(p + k);
+    for (int k = 0; k < kVecs; ++k) v[k] = __builtin_nontemporal_load(p + k * kThreads);
+    return;
+  }
 #pragma unroll
-      for (int k = 0; k < kPerThread / 4; ++k)
-        m = max(max(m, max(abs_bits(v[k].x), abs_bits(v[k].y))), max(abs_bits(v[k].z), abs_bits(v[k].w)));
+  for (int k = 0; k < kVecs; ++k) {
+    const int64_t i = base + 4 * ((int64_t)k * kThreads + threadIdx.x);
+    if (i + 4 <= n) {
+      v[k] = *reinterpret_cast<const f32x4*>(x + i);
     } else {
-      for (int64_t i = i0; i < i0 + kPerThread && i < n; ++i) m = max(m, abs_bits(x[i]));
+      v[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      if (i < n) v[k].x = x[i];
+      if (i + 1 < n) v[k].y = x[i + 1];
+      if (i + 2 < n) v[k].z = x[i + 2];
     }
   }
-  m = block_max_u32(m, lds);
-  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__device__ __forceinline__ unsigned chunk_max(const f32x4 (&v)[kVecs], unsigned m) {
+#pragma unroll
+  for (int k = 0; k < kVecs; ++k)
+    m = max(max(m, max(abs_bits(v[k].x), abs_bits(v[k].y))), max(abs_bits(v[k].z), abs_bits(v[k].w)));
+  return m;
 }
 
 // Two fp32 values to e4m3 bytes (round to nearest even) in bytes 0-1 (kHi false) or 2-3
@@ -80,44 +100,111 @@ __device__ __forceinline__ float scaled(float v, float scale) {
   return s < -448.0f ? -448.0f : (s > 448.0f ? 448.0f : s);
 }
 
-template <bool kVec>
-__global__ __launch_bounds__(kThreads) void qz_cast(const float* __restrict__ x, int64_t n,
-                                                    const unsigned* __restrict__ partial, int nparts,
-                                                    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
-  __shared__ unsigned lds[kThreads / kWave];
-  unsigned m = 0u;
-  for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
-  m = block_max_u32(m, lds);
-  const float amax = __uint_as_float(m);
-  // Python: max(amax, 1e-9) keeps a NaN amax; 448 / it in fp64, then np.float32.
-  const double den = (m > 0x7F800000u) ? (double)amax : fmax((double)amax, 1e-9);
-  const float scale = (float)(448.0 / den);
-  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+// Four fp32 values, scaled and clamped, to e4m3 codes packed in one 32-bit word.
+__device__ __forceinline__ unsigned cvt4(f32x4 v, float scale) {
+  const unsigned w = cvt2<false>(scaled(v.x, scale), scaled(v.y, scale), 0u);
+  return cvt2<true>(scaled(v.z, scale), scaled(v.w, scale), w);
+}
 
-  const int64_t stride = (int64_t)gridDim.x * kThreads * kPerThread;
-  for (int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * kPerThread; i0 < n; i0 += stride) {
-    if (kVec && i0 + kPerThread <= n) {
-      const f32x4* p = reinterpret_cast<const f32x4*>(x + i0);
-      f32x4 v[kPerThread / 4];
+// fp32 scale from the max bits: Python's max(amax, 1e-9) keeps a NaN amax; 448 / it is
+// evaluated in fp64 and rounded once to fp32.
+__device__ __forceinline__ float scale_from(unsigned m) {
+  const float amax = __uint_as_float(m);
+  const double den = (m > 0x7F800000u) ? (double)amax : fmax((double)amax, 1e-9);
+  return (float)(448.0 / den);
+}
+
+// Codes of this thread's part of the chunk at `base` (q 4-byte aligned).
+__device__ __forceinline__ void store_chunk(uint8_t* __restrict__ q, int64_t n, int64_t base,
+                                            const f32x4 (&v)[kVecs], float scale) {
+  if (base + kChunk <= n) {
+    unsigned* out = reinterpret_cast<unsigned*>(q + base) + threadIdx.x;
 #pragma unroll
-      for (int k = 0; k < kPerThread / 4; ++k) v[k] = __builtin_nontemporal_load(p + k);
-      u32x4 out;
+    for (int k = 0; k < kVecs; ++k) out[k * kThreads] = cvt4(v[k], scale);
+    return;
+  }
 #pragma unroll
-      for (int k = 0; k < kPerThread / 4; ++k) {
-        unsigned w = cvt2<false>(scaled(v[k].x, scale), scaled(v[k].y, scale), 0u);
-        w = cvt2<true>(scaled(v[k].z, scale), scaled(v[k].w, scale), w);
-        out[k] = w;
-      }
-      *reinterpret_cast<u32x4*>(q + i0) = out;
+  for (int k = 0; k < kVecs; ++k) {
+    const int64_t i = base + 4 * ((int64_t)k * kThreads + threadIdx.x);
+    const unsigned w = cvt4(v[k], scale);
+    if (i + 4 <= n) {
+      *reinterpret_cast<unsigned*>(q + i) = w;
     } else {
-      for (int64_t i = i0; i < i0 + kPerThread && i < n; ++i)
-        q[i] = (uint8_t)(cvt2<false>(scaled(x[i], scale), 0.0f, 0u) & 0xFFu);
+      for (int c = 0; c < 3; ++c)
+        if (i + c < n) q[i + c] = (uint8_t)(w >> (8 * c));
     }
   }
 }
 
-int grid_for(int64_t n, int per_cu) {
-  const int64_t per_block = (int64_t)kThreads * kPerThread;
+// ---------------------------------------------------------------------------------------
+// Aligned kernels: x 16-byte aligned (and q 4-byte aligned for the cast).
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void qz_amax(const float* __restrict__ x, int64_t n,
+                                                    unsigned* __restrict__ partial) {
+  __shared__ unsigned lds[kThreads / kWave];
+  unsigned m = 0u;
+  for (int64_t base = (int64_t)blockIdx.x * kChunk; base < n; base += (int64_t)gridDim.x * kChunk) {
+    f32x4 v[kVecs];
+    load_chunk(x, n, base, v);
+    m = chunk_max(v, m);
+  }
+  m = block_max_u32(m, lds);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void qz_cast(const float* __restrict__ x, int64_t n,
+                                                    const unsigned* __restrict__ partial, int nparts,
+                                                    uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+  __shared__ unsigned lds[kThreads / kWave];
+  int64_t base = (int64_t)blockIdx.x * kChunk;
+  // The first chunk's loads go out before the partials are read, so the two overlap.
+  f32x4 v[kVecs];
+  if (base < n) load_chunk(x, n, base, v);
+  unsigned m = 0u;
+  for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
+  m = block_max_u32(m, lds);
+  const float scale = scale_from(m);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  if (base >= n) return;
+  store_chunk(q, n, base, v, scale);
+  for (base += (int64_t)gridDim.x * kChunk; base < n; base += (int64_t)gridDim.x * kChunk) {
+    load_chunk(x, n, base, v);
+    store_chunk(q, n, base, v, scale);
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// Unaligned kernels (element loads and byte stores), for any x and q.
+// ---------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void qz_amax_any(const float* __restrict__ x, int64_t n,
+                                                        unsigned* __restrict__ partial) {
+  __shared__ unsigned lds[kThreads / kWave];
+  unsigned m = 0u;
+  const int64_t stride = (int64_t)gridDim.x * kThreads * kPerThread;
+  for (int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * kPerThread; i0 < n; i0 += stride)
+    for (int64_t i = i0; i < i0 + kPerThread && i < n; ++i) m = max(m, abs_bits(x[i]));
+  m = block_max_u32(m, lds);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
+__global__ __launch_bounds__(kThreads) void qz_cast_any(const float* __restrict__ x, int64_t n,
+                                                        const unsigned* __restrict__ partial, int nparts,
+                                                        uint8_t* __restrict__ q, float* __restrict__ scale_out) {
+  __shared__ unsigned lds[kThreads / kWave];
+  unsigned m = 0u;
+  for (int i = threadIdx.x; i < nparts; i += kThreads) m = max(m, partial[i]);
+  m = block_max_u32(m, lds);
+  const float scale = scale_from(m);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  const int64_t stride = (int64_t)gridDim.x * kThreads * kPerThread;
+  for (int64_t i0 = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * kPerThread; i0 < n; i0 += stride)
+    for (int64_t i = i0; i < i0 + kPerThread && i < n; ++i)
+      q[i] = (uint8_t)(cvt2<false>(scaled(x[i], scale), 0.0f, 0u) & 0xFFu);
+}
+
+// Workgroups for n elements at `per_block` elements per step: enough for one step each,
+// at most `per_cu` per CU and kMaxPartials.
+int grid_for(int64_t n, int64_t per_block, int per_cu) {
   int64_t g = (n + per_block - 1) / per_block;
   const int64_t cap = (int64_t)device_cu_count() * per_cu;
   if (g > cap) g = cap;
@@ -139,18 +226,22 @@ extern "C" hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* 
   if (e != hipSuccess) return e;
   auto* partial = static_cast<unsigned*>(wsp);
   const bool vx = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
-  const bool vq = (reinterpret_cast<uintptr_t>(q) & 15) == 0;
-  const int g1 = grid_for(n, 4);
-  if (vx)
-    hipLaunchKernelGGL((qz_amax<true>), dim3(g1), dim3(kThreads), 0, stream, x, n, partial);
-  else
-    hipLaunchKernelGGL((qz_amax<false>), dim3(g1), dim3(kThreads), 0, stream, x, n, partial);
+  const bool vq = (reinterpret_cast<uintptr_t>(q) & 3) == 0;
+  if (vx && vq) {
+    // With 64 floats per thread in registers, 4 workgroups per CU are resident (qz_cast
+    // holds 110 VGPRs); 1024 workgroups cover 4096 x 4096 in one chunk each.
+    const int g = grid_for(n, kChunk, 4);
+    hipLaunchKernelGGL(qz_amax, dim3(g), dim3(kThreads), 0, stream, x, n, partial);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(qz_cast, dim3(g), dim3(kThreads), 0, stream, x, n, partial, g, q, scale);
+    return hipGetLastError();
+  }
+  const int g1 = grid_for(n, (int64_t)kThreads * kPerThread, 4);
+  hipLaunchKernelGGL(qz_amax_any, dim3(g1), dim3(kThreads), 0, stream, x, n, partial);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int g2 = grid_for(n, 8);
-  if (vx && vq)
-    hipLaunchKernelGGL((qz_cast<true>), dim3(g2), dim3(kThreads), 0, stream, x, n, partial, g1, q, scale);
-  else
-    hipLaunchKernelGGL((qz_cast<false>), dim3(g2), dim3(kThreads), 0, stream, x, n, partial, g1, q, scale);
+  const int g2 = grid_for(n, (int64_t)kThreads * kPerThread, 8);
+  hipLaunchKernelGGL(qz_cast_any, dim3(g2), dim3(kThreads), 0, stream, x, n, partial, g1, q, scale);
   return hipGetLastError();
 }

@@ -23,7 +23,8 @@ import sqlite3
 import statistics
 import sys
 
-# Dominant kernel of each bench workload (a substring of the mangled kernel name).
+# Dominant kernel of each bench workload (a substring of the mangled kernel name); a
+# tuple names the kernels one call launches, whose traffic is summed.
 DOMINANT = {
     "reward_to_go": "reward_to_go_kernel",
     "pow_abs_sqrt_mean": "pow_abs_sqrt_mean_kernel",
@@ -32,6 +33,7 @@ DOMINANT = {
     "efficient_kan": "kan_gemm",
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny",
+    "quantize_e4m3": ("qz_amax", "qz_cast"),
 }
 COPY_PROBE_BYTES = 256 << 20
 
@@ -123,13 +125,17 @@ def print_traffic(t: dict) -> None:
 
 def dominant_traffic(t: dict) -> dict:
     out = {}
-    for op, sub in DOMINANT.items():
-        hits = [r for k, r in t["kernels"].items() if sub in k and "copy" not in k.lower()]
-        if not hits:
-            continue
-        fb = statistics.mean(r["fetch_bytes"] or 0.0 for r in hits)
-        wb = statistics.mean(r["write_bytes"] or 0.0 for r in hits)
-        out[op] = int(round(fb + wb))
+    for op, subs in DOMINANT.items():
+        total, found = 0.0, True
+        for sub in (subs,) if isinstance(subs, str) else subs:
+            hits = [r for k, r in t["kernels"].items() if sub in k and "copy" not in k.lower()]
+            if not hits:
+                found = False
+                break
+            total += statistics.mean(r["fetch_bytes"] or 0.0 for r in hits)
+            total += statistics.mean(r["write_bytes"] or 0.0 for r in hits)
+        if found:
+            out[op] = int(round(total))
     return out
 
 

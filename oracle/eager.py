@@ -86,6 +86,13 @@ def fp8_linear(inp: dict) -> dict:
     return {"output": (x @ w.t() + inp["bias"].to(torch.float32)).to(torch.bfloat16)}
 
 
+def quantize_e4m3(inp: dict) -> dict:
+    """tasks/fp8_linear/reference.py:15-18 (`_quantize`): max |x|, fp32 scale, clamp, cast."""
+    x = inp["x"]
+    scale = float(torch.tensor(448.0 / max(x.abs().max().item(), 1e-9), dtype=torch.float32))
+    return {"q": (x * scale).clamp(-448.0, 448.0).to(torch.float8_e4m3fn), "scale": scale}
+
+
 _FNS = {
     "pow_abs_sqrt_mean": pow_abs_sqrt_mean,
     "leaky": leaky,
@@ -93,6 +100,7 @@ _FNS = {
     "ppo_clip": ppo_clip,
     "efficient_kan": efficient_kan,
     "fp8_linear": fp8_linear,
+    "quantize_e4m3": quantize_e4m3,
 }
 
 

@@ -84,8 +84,10 @@ def _run_gpu(lib, x: torch.Tensor, q_off: int = 0, x_off: int = 0):
     return qd.cpu().numpy(), np.float32(sd.item())
 
 
+# One workgroup of the fused path holds 16384 elements; tensors above its resident capacity
+# (about 20M elements) and unaligned ones take the two-pass path.
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 65537, 1 << 20])
+@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 16384, 16385, 49151, 65537, 1 << 20, 24_000_001])
 def test_gpu_quantize_sizes(lib, n):
     print(f"\n[parity] quantize_e4m3 n={n}", flush=True)
     x = torch.randn(n, generator=torch.Generator().manual_seed(n)) * 3.0
@@ -106,7 +108,7 @@ def test_gpu_quantize_cast_table(lib):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("case", ["nan", "zeros", "inf", "unaligned"])
+@pytest.mark.parametrize("case", ["nan", "zeros", "inf", "unaligned", "q_off4", "q_off2"])
 def test_gpu_quantize_edges(lib, case):
     print(f"\n[parity] quantize_e4m3 {case}", flush=True)
     g = torch.Generator().manual_seed(5)
@@ -118,8 +120,10 @@ def test_gpu_quantize_edges(lib, case):
         x = torch.zeros(4099)
     elif case == "inf":
         x[17] = float("-inf")
-    else:
+    elif case == "unaligned":
         q_off, x_off = 3, 1
+    else:
+        q_off = int(case[-1])
     q, s = _run_gpu(lib, x, q_off=q_off, x_off=x_off)
     q_want, s_want = e4m3.quantize(x.numpy())
     assert (np.isnan(s) and np.isnan(s_want)) or s == s_want
@@ -145,3 +149,25 @@ def test_gpu_quantize_empty_writes_nothing(lib):
                                          q=torch.empty(0, dtype=torch.uint8, device="cuda"), scale=sd))
     torch.cuda.synchronize()
     assert sd.item() == -7.0
+
+
+@pytest.mark.gpu
+def test_gpu_quantize_back_to_back(lib):
+    """Calls queued without a host sync between them, a NaN tensor among them: the grid
+    barrier's state must start clean each call (a NaN max left over would poison the next)."""
+    g = torch.Generator().manual_seed(77)
+    xs = [torch.randn(300_000, generator=g) * 2.0, torch.randn(300_000, generator=g),
+          torch.randn(70_000, generator=g) * 50.0, torch.randn(5, generator=g)]
+    xs[1][123] = float("nan")
+    dev = [x.to("cuda") for x in xs]
+    qs = [torch.empty(x.numel(), dtype=torch.uint8, device="cuda") for x in xs]
+    ss = [torch.empty(1, device="cuda") for _ in xs]
+    for _ in range(2):
+        for x, q, s in zip(dev, qs, ss):
+            capi.call(lib, "quantize_e4m3", dict(x=x, n=x.numel(), q=q, scale=s))
+    torch.cuda.synchronize()
+    for x, q, s in zip(xs, qs, ss):
+        q_want, s_want = e4m3.quantize(x.numpy())
+        got = np.float32(s.item())
+        assert (np.isnan(got) and np.isnan(s_want)) or got == s_want
+        assert e4m3.same_codes(q.cpu().numpy(), q_want)
