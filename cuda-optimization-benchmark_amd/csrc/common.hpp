@@ -102,9 +102,8 @@ enum WorkspaceSlot : int {
   kSlotPow = 0,
   kSlotPpo = 1,
   kSlotKan = 2,
-  kSlotFp8 = 3,
-  kSlotQuant = 4,
-  kNumSlots = 5,
+  kSlotQuant = 3,
+  kNumSlots = 4,
 };
 
 // Returns a zero-initialised device buffer of at least `bytes` for `slot` on the current
