@@ -1,5 +1,6 @@
-"""Build libtaskops.so (all kernels + the C ABI of include/taskops.h) and the per-op
-drop-in libraries for gfx950 with hipcc, in-tree under `lib/`.
+"""Build libtaskops.so (all kernels + the C ABI of include/taskops.h), the per-op
+drop-in libraries for gfx950 with hipcc, and the HIP call counter (libhipcount.so, gcc),
+in-tree under `lib/`.
 
     __graft_entry__.build()   (the package directory name is not an importable identifier;
                                __graft_entry__.load_package() imports it as `cob_amd`)
@@ -55,6 +56,11 @@ KERNEL_SOURCES = [
 
 OPS = ["pow_abs_sqrt_mean", "leaky", "reward_to_go", "ppo_clip", "efficient_kan", "fp8_linear"]
 
+# The HIP call counter is host code only: gcc, HIP headers, no HIP runtime link.
+CC = os.environ.get("CC", "gcc")
+COUNTER_CFLAGS = ["-O2", "-std=gnu11", "-shared", "-fPIC", "-Wall", "-Wno-deprecated-declarations",
+                  "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include"]
+
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
     r = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
@@ -103,8 +109,11 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
 
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_dropin, OPS))
+    counter = LIB / "libhipcount.so"
+    _run([CC, *COUNTER_CFLAGS, str(CSRC / "callcount.c"), "-o", str(LIB / "libhipcount.so.tmp"), "-ldl"])
+    os.replace(LIB / "libhipcount.so.tmp", counter)
     if verbose:
-        print(f"built {lib} and {len(OPS)} drop-in libraries", flush=True)
+        print(f"built {lib}, {len(OPS)} drop-in libraries and {counter.name}", flush=True)
     return lib
 
 
