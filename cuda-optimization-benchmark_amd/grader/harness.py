@@ -91,7 +91,7 @@ class DropIn:
         self.fn(arr)
 
 
-def _buffers(task, op, inp):
+def _buffers(task, op, inp, device="cuda"):
     bufs, outs = {}, []
     shapes = output_shapes(op, inp)
     for ctype, name in task["params"]:
@@ -102,12 +102,12 @@ def _buffers(task, op, inp):
             n = 1
             for s in shape:
                 n *= s
-            bufs[name] = Guarded(n * torch.empty((), dtype=dt).element_size(), dt, shape)
+            bufs[name] = Guarded(n * torch.empty((), dtype=dt).element_size(), dt, shape, device)
             outs.append(name)
         else:
             x = inp[name]
             dt = torch.uint8 if x.dtype == torch.float8_e4m3fn else x.dtype
-            bufs[name] = Guarded(x.numel() * x.element_size(), dt, list(x.shape))
+            bufs[name] = Guarded(x.numel() * x.element_size(), dt, list(x.shape), device)
     return bufs, outs
 
 
@@ -120,24 +120,31 @@ def _load_set(bufs, outs, inp):
     return {k: v for k, v in inp.items() if not isinstance(v, torch.Tensor)}
 
 
-def check(op: str, case: dict, exact, kernel: DropIn | None = None) -> dict:
+def _sync(device: str) -> None:
+    if device != "cpu":
+        torch.cuda.synchronize()
+
+
+def check(op: str, case: dict, exact, kernel: DropIn | None = None, device: str = "cuda") -> dict:
     """The three-call protocol for one case; `exact(op, inputs) -> {name: array}` is the
-    checker.  Returns a record shaped like the reference's per-case log."""
+    checker.  Returns a record shaped like the reference's per-case log.  `kernel` is
+    anything with DropIn's bind/call interface; device="cpu" puts the guarded buffers in
+    host memory (for CPU kernels, such as the planted controls)."""
     task = load_task(op)
     k = kernel or DropIn(op)
     sets = [make_inputs(op, case, int(case["seed"]) + s) for s in (0, SET_B)]
-    bufs, outs = _buffers(task, op, sets[0])
+    bufs, outs = _buffers(task, op, sets[0], device)
     res = {"mode": "check", "case": case["name"], "calls": []}
     got = {}
     for call, which in ((1, 0), (2, 1), (3, 0)):
         scalars = _load_set(bufs, outs, sets[which])
-        torch.cuda.synchronize()
+        _sync(device)
         arr, keep = k.bind(bufs, scalars)
         t0 = time.time()
         k(arr)
         rec = {"call": call, "host_ms": round((time.time() - t0) * 1e3, 4)}
         try:
-            torch.cuda.synchronize()
+            _sync(device)
         except RuntimeError as e:  # the context is gone: record and stop
             rec["cuda_error"] = str(e)[:300]
             res["calls"].append(rec)
