@@ -9,8 +9,8 @@ hipEvent timing (the HIP counterpart of graders/child.py).
   guards and the inputs are checked, and calls 1 and 2 are compared with the injected
   `exact` checker under the task tolerance.  Identical bits on call 3 are reported.
 - events(): median ms per call from hipEvents around back-to-back calls (child.py:228-244);
-  a rotating set of input copies gives a cache-cold variant (the 256 MiB Infinity Cache
-  would otherwise hold inputs of up to that size between calls).
+  timing() runs it in interleaved rounds for the kernel and the PyTorch eager reference
+  (child.py:247-265).
 
 The kernel is reached the way the reference's grader reaches it: `grader_entry(void**)`
 of the op's drop-in library (lib/dropin_<op>.so), with argument addresses bound from the
@@ -125,11 +125,14 @@ def _sync(device: str) -> None:
         torch.cuda.synchronize()
 
 
-def check(op: str, case: dict, exact, kernel: DropIn | None = None, device: str = "cuda") -> dict:
+def check(op: str, case: dict, exact, kernel: DropIn | None = None, device: str = "cuda",
+          counter=None) -> dict:
     """The three-call protocol for one case; `exact(op, inputs) -> {name: array}` is the
     checker.  Returns a record shaped like the reference's per-case log.  `kernel` is
     anything with DropIn's bind/call interface; device="cpu" puts the guarded buffers in
-    host memory (for CPU kernels, such as the planted controls)."""
+    host memory (for CPU kernels, such as the planted controls).  `counter(fn) -> dict`,
+    when given, counts the HIP calls of each kernel call into the record's `count`
+    (child.py:172-178; see callcount.py)."""
     task = load_task(op)
     k = kernel or DropIn(op)
     sets = [make_inputs(op, case, int(case["seed"]) + s) for s in (0, SET_B)]
@@ -141,8 +144,10 @@ def check(op: str, case: dict, exact, kernel: DropIn | None = None, device: str 
         _sync(device)
         arr, keep = k.bind(bufs, scalars)
         t0 = time.time()
-        k(arr)
+        count = counter(lambda: k(arr)) if counter else k(arr)
         rec = {"call": call, "host_ms": round((time.time() - t0) * 1e3, 4)}
+        if counter:
+            rec["count"] = count
         try:
             _sync(device)
         except RuntimeError as e:  # the context is gone: record and stop
@@ -162,6 +167,29 @@ def check(op: str, case: dict, exact, kernel: DropIn | None = None, device: str 
     res["proc"] = "ok"
     res["finished"] = True
     return res
+
+
+def timing(op: str, case: dict, torch_ref=None, kernel: DropIn | None = None, rounds: int = 3) -> dict:
+    """Median ms per call of the kernel and, when `torch_ref(op, inputs)` is given, of the
+    PyTorch eager reference on the same device inputs: `rounds` rounds, each timing every
+    side with events() in turn, then the median over rounds and the spread (max/min - 1)
+    (child.py:247-265).  The kernel runs on guarded buffers, as in check()."""
+    task = load_task(op)
+    k = kernel or DropIn(op)
+    inp = make_inputs(op, case, int(case["seed"]))
+    bufs, outs = _buffers(task, op, inp)
+    scalars = _load_set(bufs, outs, inp)
+    arr, keep = k.bind(bufs, scalars)
+    sides = {"kernel": lambda: k(arr)}
+    if torch_ref is not None:
+        dev = {n: (v.to("cuda") if isinstance(v, torch.Tensor) else v) for n, v in inp.items()}
+        sides["torch"] = lambda: torch_ref(op, dev)
+    per_round = [{n: events(f)[0] for n, f in sides.items()} for _ in range(rounds)]
+    med = {n: statistics.median(r[n] for r in per_round) for n in sides}
+    spread = {n: (max(r[n] for r in per_round) / min(r[n] for r in per_round) - 1)
+              if min(r[n] for r in per_round) > 0 else None for n in sides}
+    return {"mode": "time", "case": case["name"], "rounds": per_round, "median_ms": med, "spread": spread,
+            "gpu": torch.cuda.get_device_name(), "torch": torch.__version__, "finished": True}
 
 
 def events(fn, min_ms: float = 1.0, batches: int = 10, warmup: int = 3):
