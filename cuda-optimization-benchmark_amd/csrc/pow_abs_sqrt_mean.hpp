@@ -16,7 +16,7 @@ namespace taskops {
 struct PowWorkspace {
   static constexpr int kMaxBlocks = 4096;
   double partial[kMaxBlocks];
-  unsigned ticket;
+  Arrivals arrivals;
 };
 
 namespace pow_detail {
@@ -77,13 +77,11 @@ __global__ __launch_bounds__(kThreads) void pow_abs_sqrt_mean_kernel(
   }
 
   const double block = block_sum<kThreads>(acc, lds);
-  if (!publish_and_arrive<1>(&ws->partial[blockIdx.x], &block, &ws->ticket, &last)) return;
-  double t = 0.0;
-  for (int j = threadIdx.x; j < (int)gridDim.x; j += kThreads) t += load_coherent(&ws->partial[j]);
+  if (!publish_and_arrive<1>(&ws->partial[blockIdx.x], &block, &ws->arrivals, &last)) return;
+  double t = gather_records<false>(ws->partial, 1, (int)gridDim.x, threadIdx.x, kThreads);
   t = block_sum<kThreads>(t, lds);
   if (threadIdx.x == 0) {
     out[0] = (float)(t / (double)n);
-    reset_ticket(&ws->ticket);
   }
 }
 

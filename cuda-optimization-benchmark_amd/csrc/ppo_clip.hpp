@@ -21,7 +21,7 @@ constexpr int kPpoFields = 7;  // gain, clipped, kl, sum r, sum r^2, sum entropy
 struct PpoWorkspace {
   static constexpr int kMaxBlocks = 4096;
   double partial[kMaxBlocks][8];
-  unsigned ticket;
+  Arrivals arrivals;
 };
 
 struct PpoParams {
@@ -162,17 +162,14 @@ __global__ __launch_bounds__(kThreads) void ppo_clip_kernel(
       t = (f == kFields - 1) ? fmax(t, lds[f][w]) : t + lds[f][w];
     rec[f] = t;
   }
-  if (!publish_and_arrive<kFields>(ws->partial[blockIdx.x], rec, &ws->ticket, &last)) return;
+  if (!publish_and_arrive<kFields>(ws->partial[blockIdx.x], rec, &ws->arrivals, &last)) return;
 
   // Finishing workgroup: wave w reduces fields w, w + waves, ... over all records (ratios
   // are positive, so 0 is the identity of the max as well as of the sums).
   __syncthreads();
   for (int f = wave; f < kFields; f += kThreads / kWave) {
-    double t = 0.0;
-    for (int j = lane; j < (int)gridDim.x; j += kWave) {
-      const double x = load_coherent(&ws->partial[j][f]);
-      t = (f == kFields - 1) ? fmax(t, x) : t + x;
-    }
+    double t = (f == kFields - 1) ? gather_records<true>(&ws->partial[0][f], 8, (int)gridDim.x, lane, kWave)
+                                  : gather_records<false>(&ws->partial[0][f], 8, (int)gridDim.x, lane, kWave);
     if (f == kFields - 1) {
 #pragma unroll
       for (int off = kWave / 2; off > 0; off >>= 1) t = fmax(t, __shfl_xor(t, off, kWave));
@@ -197,7 +194,6 @@ __global__ __launch_bounds__(kThreads) void ppo_clip_kernel(
       out[6] = (float)me;
       out[7] = (float)(-(double)coef * me);
     }
-    reset_ticket(&ws->ticket);
   }
 }
 

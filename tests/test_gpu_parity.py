@@ -235,3 +235,41 @@ def test_non_default_stream(lib):
     s.synchronize()
     r = compare(out.cpu(), exact.reward_to_go(inp)["output"], tasks.load_task("reward_to_go")["tolerance"])
     assert r["bad"] == 0, r
+
+
+# Grids of the single-launch reductions: one workgroup per 2048 elements for pow (256
+# threads x 2 x f32x4) and per 4096 for ppo_clip (512 x 2 x f32x4), capped at 512 and 256.
+# The sizes give grids of 1, fewer than the 16 arrival groups, uneven group sizes, and the
+# caps; each runs twice back to back (the arrival counters must be left zero).
+GRID_SIZES = [1, 2, 15, 16, 17, 31, 33, 100, 255, 256, 257, 511, 512, 600]
+
+
+@pytest.mark.parametrize("grid", GRID_SIZES)
+def test_grid_reduction_sizes(lib, grid):
+    print(f"\n[parity] grid reduction grid={grid}", flush=True)
+    n = grid * 2048 - 5
+    case = dict(name="g", seed=1000 + grid, batch_size=1, height=1, width=n // 4)
+    inp = inputs.make_inputs("pow_abs_sqrt_mean", case)
+    want = float(exact.pow_abs_sqrt_mean(inp)["output"])
+    args = capi.device_args("pow_abs_sqrt_mean", inp)
+    outs = [torch.full((1,), float("nan"), device="cuda") for _ in range(2)]
+    for o in outs:
+        capi.call(lib, "pow_abs_sqrt_mean", dict(args, output=o))
+    torch.cuda.synchronize()
+    for o in outs:
+        assert abs(o.item() - want) <= 1e-5 * want
+
+    m = grid * 4096 - 3
+    pcase = dict(name="g", seed=2000 + grid, B=1, T=m, H=1)
+    pinp = inputs.make_inputs("ppo_clip", pcase)
+    pwant = exact.ppo_clip(pinp)["output"]
+    pargs = capi.device_args("ppo_clip", pinp)
+    pouts = [torch.full((6,), float("nan"), device="cuda") for _ in range(2)]
+    for o in pouts:
+        capi.call(lib, "ppo_clip", dict(pargs, output=o))
+    torch.cuda.synchronize()
+    tol = tasks.load_task("ppo_clip")["tolerance"]
+    for o in pouts:
+        s = compare(o.cpu(), pwant, tol)
+        assert s["bad"] == 0, s
+    assert torch.equal(pouts[0], pouts[1])
