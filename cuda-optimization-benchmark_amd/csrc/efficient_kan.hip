@@ -5,6 +5,8 @@
 // order 3 with at most 16 knots per feature — one launch that prepares the weights and
 // basis tables, and one fused fp16x3 MFMA GEMM.  Other shapes take the row-wise fp32 path
 // below.
+#include <algorithm>
+
 #include "efficient_kan.hpp"
 
 namespace taskops {
@@ -82,34 +84,50 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
   const int table_blocks = (ngroups * kGroup * L + 255) / 256;  // one thread per table entry
+  // Split-K when the output tiles leave CUs idle (one workgroup fills a CU's LDS): up to
+  // CUs / tiles splits of the feature groups, none empty.
+  const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
+  int nsplit = 1, gper = ngroups;
+  if (tiles * 2 <= device_cu_count() && ngroups > 1) {
+    const int want = std::min(ngroups, device_cu_count() / tiles);
+    gper = (ngroups + want - 1) / want;
+    nsplit = (ngroups + gper - 1) / gper;
+  }
+  const size_t partial_bytes = nsplit > 1 ? (size_t)nsplit * tiles * BM * BN * sizeof(float) : 0;
+  const size_t fixed = 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float) + (size_t)table_blocks * sizeof(int);
+  const size_t counters_at = (fixed + 255) / 256 * 256;
+  const size_t partial_at = counters_at + ((size_t)tiles * sizeof(unsigned) + 255) / 256 * 256;
   void* wsp = nullptr;
-  hipError_t e = workspace(kSlotKan, 2 * half_bytes + table_bytes + (size_t)Opad * sizeof(float) +
-                                         (size_t)table_blocks * sizeof(int), stream, &wsp);
+  hipError_t e = workspace(kSlotKan, partial_at + partial_bytes, stream, &wsp);
   if (e != hipSuccess) return e;
   auto* bhi = static_cast<_Float16*>(wsp);
   auto* blo = reinterpret_cast<_Float16*>(static_cast<char*>(wsp) + half_bytes);
   auto* tables = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes);
   auto* colscale = reinterpret_cast<float*>(static_cast<char*>(wsp) + 2 * half_bytes + table_bytes);
   auto* uflags = reinterpret_cast<int*>(colscale + Opad);
+  auto* counters = reinterpret_cast<unsigned*>(static_cast<char*>(wsp) + counters_at);
+  auto* partial = reinterpret_cast<float*>(static_cast<char*>(wsp) + partial_at);
   // One launch finds the column scales; the next packs the weights and builds the basis
   // tables and their uniform-grid flags.
-  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, colscale);
+  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, colscale, counters,
+                     nsplit > 1 ? tiles : 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kan_pack<kCp>, dim3(table_blocks + (Opad / kPackCols) * ngroups), dim3(256), 0, stream, wb,
                      ws, sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
   const size_t lds = (size_t)kStages * kStageBytes + kTblBytes;
   const bool vec = (O % 4) == 0 && (I % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, uflags,
-                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles * nsplit), dim3(kThreads), lds, stream, x, tables, uflags,
+                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper, partial,
+                       counters);
   else
-    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles), dim3(kThreads), lds, stream, x, tables, uflags,
-                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles * nsplit), dim3(kThreads), lds, stream, x, tables, uflags,
+                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper, partial,
+                       counters);
   return hipGetLastError();
 }
 

@@ -138,12 +138,15 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 // [2^14, 2^15), so neither fp16 half under- or overflows.
 // ---------------------------------------------------------------------------------------
 // kan_prepare: workgroup o reduces column o (contiguous rows of wb, sc and ws) to
-// colscale[o].
+// colscale[o].  Workgroup 0 also zeroes kan_gemm's split-K arrival counters (their place in
+// the workspace moves with the shape, so every call starts them from zero).
 __global__ __launch_bounds__(256) void kan_prepare(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
-    int O, int C, float* __restrict__ colscale) {
+    int O, int C, float* __restrict__ colscale, unsigned* __restrict__ counters, int ncounters) {
   __shared__ float red[4];
   const int o = blockIdx.x;
+  if (o == 0)
+    for (int i = threadIdx.x; i < ncounters; i += 256) counters[i] = 0u;
   float mx = 0.0f;
   if (o < O) {
     // max_c |ws * s| = |s| * max_c |ws| exactly (rounding is monotonic).  Features are
@@ -466,19 +469,28 @@ __device__ __forceinline__ void tab_finish(float x, const TabFetch& t, int b0, f
 
 // kVec: O and I multiples of 4 and out, x 16-byte aligned (16-byte output stores and x
 // loads); otherwise 4-byte ones.  kUniform: every knot row passed kan_knots_uniform.
+//
+// Split-K (nsplit > 1, for grids of fewer tiles than CUs): workgroup b computes split
+// b % nsplit, feature groups [split*gper, split*gper + gper), of tile b / nsplit.  It
+// writes its fp32 partial tile to `partial` and arrives on the tile's counter; the last
+// of the tile's nsplit arrivals sums the partials in split order (so the result does not
+// depend on which arrives last) and writes the output.
 template <int kCp, bool kVec, bool kUniform>
 __device__ __forceinline__ void kan_gemm_body(
     uint8_t* smem, const float* __restrict__ x, const float* __restrict__ tables, int B, int I, int O,
     int L, int ngroups, int Opad, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
-    const float* __restrict__ colscale, float* __restrict__ out) {
+    const float* __restrict__ colscale, float* __restrict__ out, int nsplit, int gper,
+    float* __restrict__ partial, unsigned* __restrict__ counters) {
   constexpr int kStages = 4;
   constexpr int kQ = 1 + kCp;                        // chunks per feature group
   constexpr int kPerStep = 2 * kGroupsPerWave;        // weight copy instructions per wave per chunk
   constexpr int kX = kCp;                             // x values per lane and row block per group
   uint8_t* tbl = smem + kStages * kStageBytes;
   const int tm = (B + BM - 1) / BM, tn = Opad / BN;
+  const int split = blockIdx.x % nsplit, tile = blockIdx.x / nsplit;
+  const int g0 = split * gper, g1 = min(ngroups, g0 + gper);
   int mt, nt;
-  tile_of(blockIdx.x, tm, tn, mt, nt);
+  tile_of(tile, tm, tn, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int nq = ngroups * kQ;
@@ -563,11 +575,11 @@ __device__ __forceinline__ void kan_gemm_body(
       silu_rb(xnext, rb, hi, lo);
   };
 
-  // Prologue: group 0's table, weight chunks 0..2, group 0's x, its silu activations.
-  dma_table(0);
+  // Prologue: group g0's table, its first 3 weight chunks, its x, its silu activations.
+  dma_table(g0);
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) dma(s);
-  prefetch(0);
+  for (int s = 0; s < kStages - 1; ++s) dma(g0 * kQ + s);
+  prefetch(g0);
   f16x8 ahi[2], alo[2];
   {
     float x0[2][kX];
@@ -582,7 +594,7 @@ __device__ __forceinline__ void kan_gemm_body(
   // vmcnt counts to 63; a smaller allowance only waits for more of the later loads.
   constexpr int kW0 = kPerStep + kXLoads > 63 ? 63 : kPerStep + kXLoads;
   constexpr int kW12 = 2 * kPerStep + kXLoads > 63 ? 63 : 2 * kPerStep + kXLoads;
-  for (int g = 0; g < ngroups; ++g) {
+  for (int g = g0; g < g1; ++g) {
     barrier_no_vm_drain();
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
@@ -695,6 +707,53 @@ __device__ __forceinline__ void kan_gemm_body(
   }
   wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
 
+  if (nsplit > 1) {
+    // This thread's 16-byte slots of the tile: (wave, rb, j, lane), so every store and
+    // load instruction of a wave covers 1 KiB of contiguous memory.
+    constexpr int kTileFloats = BM * BN;
+    auto slot = [&](int rb, int j) { return (((wave * 2 + rb) * kNJ + j) * kWave + lane) * 4; };
+    const int tiles = gridDim.x / nsplit;
+    float* mine = partial + ((size_t)split * tiles + tile) * kTileFloats;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) *reinterpret_cast<f32x4*>(mine + slot(rb, j)) = acc[rb][j];
+    __syncthreads();  // every wave's stores have completed to L2; the LDS ring is idle
+    unsigned* flag = reinterpret_cast<unsigned*>(smem);
+    if (tid == 0) {
+      // Release at agent scope (writes the partial back past this XCD's L2), then arrive.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const unsigned prev = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = prev == (unsigned)nsplit - 1;
+    }
+    __syncthreads();
+    if (!*flag) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const size_t split_stride = (size_t)tiles * kTileFloats;
+    const float* first = partial + (size_t)tile * kTileFloats;
+    // Split by split, all 32 of the thread's slots at once, so the loads of a split are in
+    // flight together; each slot sums splits 0, 1, ... in order, this workgroup's own split
+    // from its registers.
+    f32x4 own[2][kNJ];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) own[rb][j] = acc[rb][j];
+    for (int sp = 0; sp < nsplit; ++sp) {
+      const float* src = first + sp * split_stride;
+      f32x4 part[2][kNJ];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j)
+          part[rb][j] = sp == split ? own[rb][j] : *reinterpret_cast<const f32x4*>(src + slot(rb, j));
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) acc[rb][j] = sp == 0 ? part[rb][j] : acc[rb][j] + part[rb][j];
+    }
+  }
+
   // Epilogue: lane holds columns n0 + 16j + 4*fg + 0..3 of batch row row0 + 16rb + fr.
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, (size_t)B * O * 4);
 #pragma unroll
@@ -728,14 +787,17 @@ template <int kCp, bool kVec>
 __global__ __launch_bounds__(kThreads) void kan_gemm(
     const float* __restrict__ x, const float* __restrict__ tables, const int* __restrict__ uflags,
     int nflags, int B, int I, int O, int L, int ngroups, int Opad, const _Float16* __restrict__ bhi,
-    const _Float16* __restrict__ blo, const float* __restrict__ colscale, float* __restrict__ out) {
+    const _Float16* __restrict__ blo, const float* __restrict__ colscale, float* __restrict__ out, int nsplit,
+    int gper, float* __restrict__ partial, unsigned* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   bool ok = true;
   for (int i = (int)threadIdx.x % kWave; i < nflags; i += kWave) ok = ok && uflags[i] != 0;
   if (__builtin_amdgcn_ballot_w64(!ok) == 0)
-    kan_gemm_body<kCp, kVec, true>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    kan_gemm_body<kCp, kVec, true>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit,
+                                   gper, partial, counters);
   else
-    kan_gemm_body<kCp, kVec, false>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out);
+    kan_gemm_body<kCp, kVec, false>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit,
+                                    gper, partial, counters);
 }
 
 }  // namespace kan
