@@ -105,6 +105,10 @@ KAN_SHAPES = [
     (70, 64, 96, 5, 3, 1.2, "jitter"),
     (21, 40, 50, 6, 2, 1.2, "random"),
     (16, 12, 8, 13, 1, 1.0, "uniform"),
+    # Split-K (fewer output tiles than CUs): 64 tiles and 5 feature groups split 2+2+1;
+    # 96 tiles, ragged O and 3 groups split 2+1.
+    (4096, 160, 512, 8, 3, 1.0, "uniform"),
+    (4096, 90, 600, 5, 3, 1.0, "random"),
 ]
 
 
