@@ -1,6 +1,6 @@
 """Build libtaskops.so (all kernels + the C ABI of include/taskops.h), the per-op
-drop-in libraries for gfx950 with hipcc, and the HIP call counter (libhipcount.so, gcc),
-in-tree under `lib/`.
+drop-in libraries for gfx950 with hipcc, the HIP call counter (libhipcount.so, gcc) and
+the torch.ops.taskops operators (libtaskops_torch.so, g++), in-tree under `lib/`.
 
     __graft_entry__.build()   (the package directory name is not an importable identifier;
                                __graft_entry__.load_package() imports it as `cob_amd`)
@@ -112,8 +112,27 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     counter = LIB / "libhipcount.so"
     _run([CC, *COUNTER_CFLAGS, str(CSRC / "callcount.c"), "-o", str(LIB / "libhipcount.so.tmp"), "-ldl"])
     os.replace(LIB / "libhipcount.so.tmp", counter)
+    ext = build_torch_ops()
     if verbose:
-        print(f"built {lib}, {len(OPS)} drop-in libraries and {counter.name}", flush=True)
+        print(f"built {lib}, {len(OPS)} drop-in libraries, {counter.name} and {ext.name}", flush=True)
     return lib
+
+
+def build_torch_ops() -> Path:
+    """lib/libtaskops_torch.so: the torch.ops.taskops operators (host C++ over the C ABI,
+    g++ against torch's headers; libtaskops.so is found next to it)."""
+    import torch
+    import torch.utils.cpp_extension as ce
+    out = LIB / "libtaskops_torch.so"
+    tmp = LIB / "libtaskops_torch.so.tmp"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    inc = [f"-I{p}" for p in ce.include_paths(device_type="cuda")]
+    libdirs = [f"-L{p}" for p in ce.library_paths(device_type="cuda")]
+    _run([os.environ.get("CXX", "g++"), "-O2", "-std=c++17", "-fPIC", "-shared", "-D__HIP_PLATFORM_AMD__",
+          f"-D_GLIBCXX_USE_CXX11_ABI={abi}", "-DTORCH_API_INCLUDE_EXTENSION_H", *inc, f"-I{INCLUDE}",
+          str(CSRC / "torch_ext" / "taskops_torch.cpp"), "-o", str(tmp), *libdirs, "-lc10", "-lc10_hip",
+          "-ltorch_cpu", "-ltorch_hip", "-lamdhip64", f"-L{LIB}", "-ltaskops", "-Wl,-rpath,$ORIGIN", "-Wl,--no-undefined"])
+    os.replace(tmp, out)
+    return out
 
 
