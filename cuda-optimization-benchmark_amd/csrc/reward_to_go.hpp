@@ -34,9 +34,10 @@ __device__ __forceinline__ double coef(unsigned word, int byte, double g) {
 
 // Output stores as buffer stores with an explicit cache policy.  Measured on MI355X at
 // B = T = 4096 (80 MB read, 64 MB written): a plain copy of the same traffic takes 31.0 us
-// with plain stores and 28.7 us with nt | sc0, but this kernel takes 38.6-39.0 us with nt
-// (with or without sc0) and 31.6 us with sc0 against 31.2 us with plain stores, so the
-// dispatch uses plain stores; policies with sc1 set take 51-68 us even in the copy.
+// with plain stores and 28.7 us with nt | sc0; policies with sc1 set take 51-68 us.  Which
+// policy pays depends on the access pattern: with 4 steps per lane (whole 1 KiB per store
+// instruction) nt stores are the fastest, with 8 steps per lane (every other 16 bytes)
+// they are the slowest (reward_to_go.hip).
 template <int kStorePolicy>  // bit 0 sc0, bit 1 nt
 __device__ __forceinline__ void store_row16(float* row_base, int T, int t, f32x4 w) {
   const __amdgpu_buffer_rsrc_t rs =

@@ -277,3 +277,21 @@ def test_grid_reduction_sizes(lib, grid):
         s = compare(o.cpu(), pwant, tol)
         assert s["bad"] == 0, s
     assert torch.equal(pouts[0], pouts[1])
+
+
+# reward_to_go's launch shape follows the row length in chunks of 256 steps: 1, 2 or 4
+# waves of one chunk, 4 waves of 2, or 4 waves of 4 (rows past 4096 steps take several
+# segments).  T values on either side of each boundary; T % 4 != 0 takes the element path.
+RTG_T = [1, 255, 256, 257, 511, 512, 513, 1023, 1024, 1025, 1500, 2048, 2049, 4095, 4096, 4097, 9000]
+
+
+@pytest.mark.parametrize("T", RTG_T)
+def test_reward_to_go_lengths(lib, T):
+    print(f"\n[parity] reward_to_go T={T}", flush=True)
+    case = dict(name="t", seed=3000 + T, B=3, T=T, gamma=0.98, done_p=0.02)
+    inp = inputs.make_inputs("reward_to_go", case)
+    want = exact.reward_to_go(inp)["output"]
+    for _ in range(2):
+        got = capi.run_op(lib, "reward_to_go", inp)["output"].cpu()
+        s = compare(got, want, tasks.load_task("reward_to_go")["tolerance"])
+        assert s["bad"] == 0, s
