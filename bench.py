@@ -166,8 +166,10 @@ def time_cpu(op, inp, budget_s=10.0, max_reps=5):
     return statistics.median(warm), len(runs)
 
 
-def _traffic():
-    p = ROOT / "profiles" / "traffic.json"
+def _profile_json(name):
+    """A {bench op key: value} summary kept under profiles/ (traffic.json: HBM bytes per
+    launch; mfma.json: MFMA busy % of the dominant kernel), or {}."""
+    p = ROOT / "profiles" / name
     if p.exists():
         try:
             return json.loads(p.read_text())
@@ -204,7 +206,8 @@ def main() -> int:
     if omp.isdigit() and int(omp) > 0:
         cores = min(cores, int(omp))
     torch.set_num_threads(cores)
-    traffic = _traffic()
+    traffic = _profile_json("traffic.json")
+    mfma_busy = _profile_json("mfma.json")
     if a.copy_probe:
         copy_probe()
     ops = [o for o in a.ops.split(",") if o]
@@ -235,6 +238,8 @@ def main() -> int:
                     "frac": round(achieved / peak, 4)}
             if dtype in MFMA_PASSES:
                 roof["ceiling_frac"] = round(1.0 / MFMA_PASSES[dtype], 4)
+            if key in mfma_busy:
+                roof["mfma_busy_pct"] = mfma_busy[key]  # rocprofv3 counters, profiles/mfma_utilisation.md
         roof["traffic"] = traffic.get(key)
         r = {"workload": desc, "us_per_call": round(us, 3), "dtype": dtype,
              "algorithmic_" + ("bytes" if bound == "hbm" else "flop"): work,

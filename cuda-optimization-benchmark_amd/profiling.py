@@ -4,6 +4,15 @@
         Per-kernel dispatch count and average / median / min / max duration from a
         `rocprofv3 --kernel-trace --stats -d DIR` run (a markdown table).
 
+    python cuda-optimization-benchmark_amd/profiling.py mfma DIR [--simds 1024] [--xcds 8]
+        MFMA utilisation per kernel from a `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES
+        SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_F8 GRBM_GUI_ACTIVE` run:
+        busy = MFMA-busy cycles summed over SIMDs / (GUI-active cycles x SIMDs), the
+        MfmaUtil expression of rocprofiler's counter definitions, and the MFMA work
+        executed per dispatch (MOPS x 512 FLOP).  The result database holds each counter
+        summed over its instances; GRBM_GUI_ACTIVE has one instance per XCD, all counting
+        the same cycles (MfmaUtil takes their maximum), so the sum is divided by the XCDs.
+
     python cuda-optimization-benchmark_amd/profiling.py traffic FETCH_DIR WRITE_DIR [--json OUT]
         Per-kernel HBM traffic per dispatch from two `rocprofv3 --pmc FETCH_SIZE` and
         `--pmc WRITE_SIZE` runs of `bench.py --copy-probe`.  Both counters (KiB per
@@ -66,16 +75,16 @@ def print_stats(d: str) -> None:
               f"| {min(v):.2f} | {max(v):.2f} |")
 
 
-def counter_values(d: str, counter: str) -> dict:
-    """kernel name -> per-dispatch counter values (summed over the counter's instances),
-    in dispatch order."""
+def counter_values(d: str, counter: str, reduce: str = "sum") -> dict:
+    """kernel name -> per-dispatch counter values (summed, or with reduce="max" the
+    largest, over the counter's instances), in dispatch order."""
     c = _db(d)
     per = collections.defaultdict(float)
     names = {}
     for name, disp, val in c.execute(
             "select kernel_name, dispatch_id, value from counters_collection where counter_name = ?",
             (counter,)):
-        per[disp] += val
+        per[disp] = max(per[disp], val) if reduce == "max" else per[disp] + val
         names[disp] = name
     agg = collections.defaultdict(list)
     for disp in sorted(per):
@@ -139,11 +148,45 @@ def dominant_traffic(t: dict) -> dict:
     return out
 
 
+MI355X_SIMDS = 256 * 4
+MI355X_XCDS = 8
+
+
+def mfma_util(d: str, simds: int = MI355X_SIMDS, xcds: int = MI355X_XCDS) -> dict:
+    """kernel -> {dispatches, busy_pct, f16_flop, f8_flop} (means over dispatches)."""
+    busy = counter_values(d, "SQ_VALU_MFMA_BUSY_CYCLES")
+    gui = {k: [v / xcds for v in vs] for k, vs in counter_values(d, "GRBM_GUI_ACTIVE").items()}
+    f16 = counter_values(d, "SQ_INSTS_VALU_MFMA_MOPS_F16")
+    f8 = counter_values(d, "SQ_INSTS_VALU_MFMA_MOPS_F8")
+    out = {}
+    for k, b in busy.items():
+        g = gui.get(k)
+        if not g or sum(b) == 0:
+            continue
+        out[k] = {"dispatches": len(b),
+                  "busy_pct": 100.0 * statistics.mean(bb / (gg * simds) for bb, gg in zip(b, g)),
+                  "f16_flop": 512.0 * statistics.mean(f16.get(k, [0.0])),
+                  "f8_flop": 512.0 * statistics.mean(f8.get(k, [0.0]))}
+    return out
+
+
+def print_mfma(u: dict) -> None:
+    print("| kernel | dispatches | MFMA busy % | fp16 MFMA FLOP / dispatch | fp8 MFMA FLOP / dispatch |")
+    print("|---|---:|---:|---:|---:|")
+    for k, r in sorted(u.items(), key=lambda kv: -kv[1]["busy_pct"]):
+        print(f"| `{_short(k)}` | {r['dispatches']} | {r['busy_pct']:.1f} | {r['f16_flop']:.4g} | {r['f8_flop']:.4g} |")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("dir")
+    m = sub.add_parser("mfma")
+    m.add_argument("dir")
+    m.add_argument("--simds", type=int, default=MI355X_SIMDS)
+    m.add_argument("--xcds", type=int, default=MI355X_XCDS)
+    m.add_argument("--json", help="write {bench op key: MFMA busy %% of its dominant kernel}")
     t = sub.add_parser("traffic")
     t.add_argument("fetch_dir")
     t.add_argument("write_dir")
@@ -151,6 +194,18 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print_stats(a.dir)
+    elif a.cmd == "mfma":
+        u = mfma_util(a.dir, a.simds, a.xcds)
+        print_mfma(u)
+        if a.json:
+            dom = {}
+            for op, sub in DOMINANT.items():
+                hits = [r["busy_pct"] for k, r in u.items() if isinstance(sub, str) and sub in k]
+                if hits:
+                    dom[op] = round(statistics.mean(hits), 1)
+            with open(a.json, "w") as fh:
+                json.dump(dom, fh, indent=1, sort_keys=True)
+                fh.write("\n")
     else:
         tr = traffic(a.fetch_dir, a.write_dir)
         print_traffic(tr)
