@@ -4,10 +4,11 @@ cuda-optimization-benchmark_amd/grader/report.py).  Not collected by pytest; run
 
     python tests/grade_gpu.py OUT_DIR [--ops a,b] [--passes 2]
 
-For each op: every hidden and public case through the three-call protocol on guarded
-buffers (grader/harness.py check()), in `--passes` passes, with the HIP call counter armed
-around each call; then the task's timed case in 3 interleaved rounds of the kernel and
-PyTorch eager on the GPU (harness.timing()).  The checker is oracle/exact.py and the eager
+For each op (grade_op()): every hidden and public case through the three-call protocol on
+guarded buffers (grader/harness.py check()), in `--passes` passes, with the HIP call counter
+armed around each call; then the task's timed case in 3 interleaved rounds of the kernel
+and PyTorch eager on the GPU (harness.timing()).  tests/test_proof_flow.py runs grade_op()
+on the CPU with planted kernels.  The checker is oracle/exact.py and the eager
 side oracle/eager.py, which is why this driver lives under tests/.  There is no expert
 kernel on this GPU, so `% of expert speed` stays empty.
 """
@@ -24,6 +25,31 @@ import __graft_entry__  # noqa: E402
 
 __graft_entry__.load_package()
 from cob_amd import callcount  # noqa: E402
+
+
+def grade_op(op, kernel, exact_fn, passes=2, counter=None, device="cuda", torch_ref=None, key=None, env=None,
+             log=print):
+    """One kernel's grading log: every hidden and public case of `op` through check() in
+    `passes` passes, then (with `torch_ref`) the timed case's timing, and the verdict."""
+    from cob_amd import tasks
+    from cob_amd.grader import harness, report
+    t0 = time.time()
+    out = {"key": key or f"taskops_{op}", "task": op, "env": env or {}, "compile": {"ok": True}, "passes": []}
+    for p in range(passes):
+        cases = []
+        for case in tasks.all_cases(op):
+            log(f"[grade] {op} pass {p + 1} {case['name']}")
+            rec = harness.check(op, case, exact_fn, kernel=kernel, device=device, counter=counter)
+            rec["name"] = case["name"]
+            cases.append(rec)
+        out["passes"].append({"cases": cases})
+    if torch_ref is not None:
+        timed = next(c for c in tasks.all_cases(op) if c.get("timed"))
+        log(f"[grade] {op} timing {timed['name']}")
+        out["timing"] = harness.timing(op, timed, torch_ref=torch_ref, kernel=kernel)
+    out["seconds"] = round(time.time() - t0, 2)
+    out["verdict"] = report.kernel_verdict(out)
+    return out
 
 
 def main(argv=None) -> int:
@@ -50,29 +76,17 @@ def main(argv=None) -> int:
            "torch": torch.__version__, "python": platform.python_version()}
     (out / "env.json").write_text(json.dumps(env, indent=1))
     for op in ops:
-        t0 = time.time()
         lib = LIB_DIR / f"dropin_{op}.so"
-        log = {"key": f"taskops_{op}", "task": op, "env": env,
-               "compile": {"ok": lib.exists(), "lib": lib.name,
-                           "log_tail": "" if lib.exists() else f"{lib} not built"}}
         if lib.exists():
-            kernel = harness.DropIn(op)
-            log["passes"] = []
-            for p in range(a.passes):
-                cases = []
-                for case in tasks.all_cases(op):
-                    print(f"[grade] {op} pass {p + 1} {case['name']}", file=sys.stderr, flush=True)
-                    rec = harness.check(op, case, exact.reference_exact, kernel=kernel,
-                                        counter=lambda fn: counter.count(fn, 0))
-                    rec["name"] = case["name"]
-                    cases.append(rec)
-                log["passes"].append({"cases": cases})
-            if not a.no_timing:
-                timed = next(c for c in tasks.all_cases(op) if c.get("timed"))
-                print(f"[grade] {op} timing {timed['name']}", file=sys.stderr, flush=True)
-                log["timing"] = harness.timing(op, timed, torch_ref=eager.reference, kernel=kernel)
-        log["seconds"] = round(time.time() - t0, 2)
-        log["verdict"] = report.kernel_verdict(log)
+            log = grade_op(op, harness.DropIn(op), exact.reference_exact, passes=a.passes,
+                           counter=lambda fn: counter.count(fn, 0),
+                           torch_ref=None if a.no_timing else eager.reference, env=env,
+                           log=lambda m: print(m, file=sys.stderr, flush=True))
+            log["compile"] = {"ok": True, "lib": lib.name, "log_tail": ""}
+        else:
+            log = {"key": f"taskops_{op}", "task": op, "env": env,
+                   "compile": {"ok": False, "lib": lib.name, "log_tail": f"{lib} not built"}}
+            log["verdict"] = report.kernel_verdict(log)
         (out / f"{log['key']}.json").write_text(json.dumps(log, indent=1))
         v = log["verdict"]
         print(f"[grade] {op}: {v['status']} {v['label'] or ''} kernel {v['kernel_ms']} ms, "
