@@ -54,6 +54,9 @@ WORKLOADS = {
               "leaky T=256 B=64 H=4096 beta=0.9 threshold=1.0"),
     "ppo_clip": ("ppo_clip", "ppo_clip", "hbm", 268_435_488, "f32",
                  "ppo_clip N=2^24 (65536x256x1) + entropy, eps=0.2, coef=0.01"),
+    # The reference's own 3-in / 6-out operator on the same inputs (no entropy stream).
+    "ppo_clip_dropin": ("ppo_clip", "ppo_clip", "hbm", 201_326_616, "f32",
+                        "ppo_clip N=2^24 (65536x256x1) drop-in: 3 inputs, 6 outputs, eps=0.2"),
     "efficient_kan": ("efficient_kan", "efficient_kan", "mfma", 154_618_822_656, "fp16x3",
                       "efficient_kan B=8192 I=O=1024 grid_size=5 spline_order=3"),
     "fp8_linear": ("fp8_linear", "fp8_linear", "mfma", 137_438_953_472, "fp8",
@@ -65,8 +68,8 @@ WORKLOADS = {
     "quantize_e4m3": ("quantize_e4m3", "fp8_linear", "hbm", 5 * 4096 * 4096, "f32",
                       "quantize_e4m3 x fp32 [4096,4096] -> e4m3 + fp32 scale (fp8_linear operand)"),
 }
-ORDER = ["reward_to_go", "pow_abs_sqrt_mean", "leaky", "ppo_clip", "efficient_kan", "fp8_linear",
-         "fp8_linear_m16", "quantize_e4m3"]
+ORDER = ["reward_to_go", "pow_abs_sqrt_mean", "leaky", "ppo_clip", "ppo_clip_dropin", "efficient_kan",
+         "fp8_linear", "fp8_linear_m16", "quantize_e4m3"]
 
 
 def _log(msg: str) -> None:
@@ -150,7 +153,17 @@ def copy_probe():
     torch.cuda.empty_cache()
 
 
-def time_cpu(op, inp, budget_s=10.0, max_reps=5):
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def time_cpu(op, inp, budget_s=10.0, max_reps=6):
     """Median seconds per call of the oracle's fp32 eager restatement on this host."""
     import torch
     from oracle import eager
@@ -217,11 +230,13 @@ def main() -> int:
         case = tasks.BASELINE[bkey]
         _log(f"[bench] {key}: generating inputs")
         inp = _quant_inputs(case) if entry == "quantize_e4m3" else inputs.make_inputs(entry, case)
+        if key == "ppo_clip_dropin":
+            inp = {k: v for k, v in inp.items() if k not in ("entropy", "entropy_coef")}
         probe = _device_sets(entry, inp, 1)
         per_set = _set_bytes(probe[0])
         n = _copies(per_set) if bound == "hbm" else 1
         sets = probe + _device_sets(entry, inp, n - 1)
-        call_entry = "ppo_clip_entropy" if entry == "ppo_clip" else entry
+        call_entry = "ppo_clip_entropy" if key == "ppo_clip" else entry
         _log(f"[bench] {key}: timing {a.steps} calls over {n} rotating copies")
         ms = time_gpu(lib, entry, call_entry, sets, a.steps, a.warmup)
         del sets, probe
@@ -276,7 +291,7 @@ def main() -> int:
         "ops": results,
         "env": {"gpu": getattr(torch.cuda.get_device_properties(0), "gcnArchName", "")
                 or torch.cuda.get_device_name(), "torch": torch.__version__,
-                "cpu": platform.processor() or platform.machine(), "cpu_threads": cores},
+                "cpu": _cpu_model(), "cpu_threads": cores},
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -38,7 +38,9 @@ DOMINANT = {
     "reward_to_go": "reward_to_go_kernel",
     "pow_abs_sqrt_mean": "pow_abs_sqrt_mean_kernel",
     "leaky": "leaky_kernel",
-    "ppo_clip": "ppo_clip_kernel",
+    # <threads, unroll, vector loads, entropy, nt>: the entropy and the drop-in variants
+    "ppo_clip": "ppo_clip_kernel<512, 2, true, true,",
+    "ppo_clip_dropin": "ppo_clip_kernel<512, 2, true, false,",
     "efficient_kan": "kan_gemm",
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny",
