@@ -88,7 +88,9 @@ EXPECTED_LAUNCHES = {
     "pow_abs_sqrt_mean": 1, "leaky": 1, "reward_to_go": 1, "ppo_clip": 1, "ppo_clip_entropy": 1,
     "efficient_kan": 3,          # kan_prepare + kan_pack + kan_gemm (spline order 3)
     "efficient_kan_rowwise": 1,  # kan_rowwise (other spline orders)
-    "fp8_linear": 1, "quantize_e4m3": 2,
+    "fp8_linear": 1,
+    "quantize_e4m3": 2,          # qz_amax + qz_cast (unaligned, or more chunks than fit at once)
+    "quantize_e4m3_fused": 1,    # qz_fused (aligned, every chunk resident at once)
 }
 
 
@@ -139,7 +141,8 @@ def workloads():
                     B=64, I=40, O=24, spline_order=order)
         out.append((f"efficient_kan/{case['name']}", "efficient_kan", "efficient_kan_rowwise",
                     drop_in("efficient_kan", case)))
-    out.append(("quantize_e4m3/aligned_n1000003", "quantize_e4m3", "quantize_e4m3", quant(1_000_003, 0)))
+    out.append(("quantize_e4m3/aligned_n1000003", "quantize_e4m3", "quantize_e4m3_fused", quant(1_000_003, 0)))
+    out.append(("quantize_e4m3/aligned_n67108864", "quantize_e4m3", "quantize_e4m3", quant(1 << 26, 0)))
     out.append(("quantize_e4m3/unaligned_n4099", "quantize_e4m3", "quantize_e4m3", quant(4099, 1)))
     return out
 

@@ -7,24 +7,29 @@
 // A NaN in x makes amax, scale and every q NaN: torch's max, Python's max(nan, 1e-9) and
 // the casts all keep it.
 //
-// Two launches over x (HBM-bound; algorithmic bytes are 4 in + 1 out per element, the
-// second read of x is the price of the global max).  qz_amax reduces |x| per workgroup
+// HBM-bound; algorithmic bytes are 4 in + 1 out per element.  The max is taken over |x|
 // as raw bits: for |x| the IEEE order is the unsigned-integer order and every NaN sorts
-// above inf, so an integer max propagates NaN; each workgroup writes one partial.
-// qz_cast reduces those partials (a few KiB from L2), derives the scale and converts
-// with v_cvt_pk_fp8_f32.
+// above inf, so an integer max propagates NaN.  Conversion is v_cvt_pk_fp8_f32.
 //
-// Both kernels walk x in chunks of 16384 elements per workgroup and step.  A thread
+// Two launches (unaligned operands, or more chunks than can be resident at once): qz_amax
+// writes one partial max per workgroup; qz_cast reduces those partials (a few KiB from L2),
+// derives the scale and converts, reading x a second time.
+//
+// The kernels walk x in chunks of 16384 elements per workgroup and step.  A thread
 // issues all 16 of its 16-byte loads of a chunk before it uses any (64 floats in
 // registers), so each wave keeps 16 KiB in flight: at one chunk per workgroup, which a
 // 4096 x 4096 operand is on 256 CUs, a kernel is one round trip of loads.  Element
 // base + 4 * (k * 256 + t) + c of a chunk belongs to thread t, so every load and store
 // instruction of a wave covers contiguous memory.
 //
-// A single launch that keeps x in registers across a grid barrier would read x once,
-// but its barrier needs every workgroup resident: a cooperative launch guarantees that
-// and costs about 100 us per launch on this stack (measured), and a plain launch does
-// not guarantee it.
+// One launch (qz_fused, when the grid fits the resident capacity): each workgroup keeps its
+// chunk in registers, the workgroups combine their maxima through a grid barrier, and each
+// converts the chunk it holds, so x is read once.  The barrier is a plain launch sized by
+// the occupancy API (a cooperative launch, which guarantees residency, costs about 100 us
+// per launch on this stack).  Residency is not guaranteed (another stream's kernels can
+// hold CUs), so the wait is bounded: a workgroup that times out reads all of x for the max
+// itself.  The max is exact and order-free, so both paths give identical bits, every wave
+// exits, and no result depends on the timing.
 #include "common.hpp"
 
 namespace taskops {
@@ -202,6 +207,128 @@ __global__ __launch_bounds__(kThreads) void qz_cast_any(const float* __restrict_
       q[i] = (uint8_t)(cvt2<false>(scaled(x[i], scale), 0.0f, 0u) & 0xFFu);
 }
 
+// ---------------------------------------------------------------------------------------
+// Fused single pass.
+// ---------------------------------------------------------------------------------------
+// Barrier words in the workspace after the partials, one per 64-byte line: group g's
+// arrival count and max, the top count and max, the published result and the sense flag.
+// Arrival is two-level (RMWs on one address serialise at the coherence point, about 12 ns
+// each): workgroup b arrives in group b % 16; a group's last arrival folds the group max
+// into the top max and arrives at the top; the top's last arrival publishes the max and
+// flips the sense.  Workgroups wait for the sense to differ from what they read at start
+// (a sense-reversal barrier): the last arrivals reset every count and max on the way, and
+// the flipped sense is the next launch's starting value, so no host reset is needed and a
+// captured graph replays correctly.
+constexpr int kQzGroups = 16;
+constexpr int kQzLine = 16;  // unsigned per 64-byte line
+enum QzWord : int { kQzGroupCount = 0, kQzGroupMax = kQzGroups, kQzTopCount = 2 * kQzGroups, kQzTopMax,
+                    kQzResult, kQzSense, kQzWords };
+constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the sense flag (~1 us each) before the fallback
+
+__device__ __forceinline__ unsigned* qz_word(unsigned* bar, int w, int i = 0) { return bar + (w + i) * kQzLine; }
+__device__ __forceinline__ unsigned qz_load(unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void qz_store(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned qz_max(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned qz_add(unsigned* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Requires x 16-byte and q 4-byte aligned and gridDim.x = ceil(n / kChunk).  Thread 0 of
+// each workgroup runs the barrier; every RMW's returned value is used before the next
+// one is issued, which orders them at the coherence point.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void qz_fused(
+    const float* __restrict__ x, int64_t n, uint8_t* __restrict__ q, float* __restrict__ scale_out,
+    unsigned* __restrict__ bar, unsigned spin_limit) {
+  __shared__ unsigned lds[kThreads / kWave];
+  __shared__ unsigned gmax_s, fallback_s;
+  const int64_t base = (int64_t)blockIdx.x * kChunk;
+  f32x4 v[kVecs];
+  load_chunk(x, n, base, v);
+  // The sense is read behind the chunk's loads; it only has to be read before this
+  // workgroup arrives.
+  unsigned sense = 0u;
+  if (threadIdx.x == 0) sense = qz_load(qz_word(bar, kQzSense));
+  const unsigned m = block_max_u32(chunk_max(v, 0u), lds);
+
+  if (threadIdx.x == 0) {
+    asm volatile("" ::"v"(sense));
+    const unsigned grid = gridDim.x, g = blockIdx.x % kQzGroups;
+    const unsigned groups = grid < kQzGroups ? grid : kQzGroups;
+    const unsigned members = grid / kQzGroups + (g < grid % kQzGroups ? 1u : 0u);
+    unsigned r = qz_max(qz_word(bar, kQzGroupMax, g), m);
+    asm volatile("" ::"v"(r));
+    if (qz_add(qz_word(bar, kQzGroupCount, g)) == members - 1) {  // the group's last arrival
+      const unsigned gm = qz_load(qz_word(bar, kQzGroupMax, g));
+      asm volatile("" ::"v"(gm));
+      qz_store(qz_word(bar, kQzGroupMax, g), 0u);
+      qz_store(qz_word(bar, kQzGroupCount, g), 0u);
+      r = qz_max(qz_word(bar, kQzTopMax), gm);
+      asm volatile("" ::"v"(r));
+      if (qz_add(qz_word(bar, kQzTopCount)) == groups - 1) {  // the grid's last arrival
+        const unsigned tm = qz_load(qz_word(bar, kQzTopMax));
+        r = __hip_atomic_exchange(qz_word(bar, kQzResult), tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(r));
+        qz_store(qz_word(bar, kQzTopMax), 0u);
+        qz_store(qz_word(bar, kQzTopCount), 0u);
+        r = __hip_atomic_exchange(qz_word(bar, kQzSense), sense ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        asm volatile("" ::"v"(r));
+      }
+    }
+    bool flipped = false;
+    for (unsigned i = 0; i < spin_limit; ++i) {
+      if (qz_load(qz_word(bar, kQzSense)) != sense) {
+        flipped = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    fallback_s = flipped ? 0u : 1u;
+    gmax_s = flipped ? qz_load(qz_word(bar, kQzResult)) : 0u;
+  }
+  __syncthreads();
+  unsigned gm = gmax_s;
+  if (fallback_s) {  // the barrier did not complete in time: this workgroup finds the max itself
+    unsigned mm = 0u;    // (one 16-byte load at a time: the chunk in v stays in registers)
+    const int64_t n4 = n & ~(int64_t)3;
+    for (int64_t i = 4 * (int64_t)threadIdx.x; i < n4; i += 4 * kThreads) {
+      const f32x4 w = *reinterpret_cast<const f32x4*>(x + i);
+      mm = max(max(mm, max(abs_bits(w.x), abs_bits(w.y))), max(abs_bits(w.z), abs_bits(w.w)));
+    }
+    if ((int64_t)threadIdx.x < n - n4) mm = max(mm, abs_bits(x[n4 + threadIdx.x]));
+    gm = block_max_u32(mm, lds);
+  }
+  const float scale = scale_from(gm);
+  if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
+  store_chunk(q, n, base, v, scale);
+}
+
+unsigned g_qz_spin_limit = kQzSpinDefault;
+int g_qz_capacity[64];  // resident qz_fused workgroups per device (0: not yet known, -1: none)
+
+int fused_capacity() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int cap = __atomic_load_n(&g_qz_capacity[dev], __ATOMIC_RELAXED);
+  if (cap != 0) return cap > 0 ? cap : 0;
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(qz_fused), kThreads, 0) !=
+          hipSuccess ||
+      per_cu <= 0) {
+    (void)hipGetLastError();
+    cap = -1;
+  } else {
+    cap = per_cu * device_cu_count();
+  }
+  __atomic_store_n(&g_qz_capacity[dev], cap, __ATOMIC_RELAXED);
+  return cap > 0 ? cap : 0;
+}
+
 // Workgroups for n elements at `per_block` elements per step: enough for one step each,
 // at most `per_cu` per CU and kMaxPartials.
 int grid_for(int64_t n, int64_t per_block, int per_cu) {
@@ -222,11 +349,17 @@ extern "C" hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* 
   if (n < 0) return hipErrorInvalidValue;
   if (n == 0) return hipSuccess;  // nothing to quantise; *scale is left as it is
   void* wsp = nullptr;
-  hipError_t e = workspace(kSlotQuant, kMaxPartials * sizeof(unsigned), stream, &wsp);
+  hipError_t e = workspace(kSlotQuant, (kMaxPartials + kQzWords * kQzLine) * sizeof(unsigned), stream, &wsp);
   if (e != hipSuccess) return e;
   auto* partial = static_cast<unsigned*>(wsp);
   const bool vx = (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   const bool vq = (reinterpret_cast<uintptr_t>(q) & 3) == 0;
+  const int64_t chunks = (n + kChunk - 1) / kChunk;
+  if (vx && vq && chunks <= fused_capacity()) {
+    hipLaunchKernelGGL(qz_fused, dim3((unsigned)chunks), dim3(kThreads), 0, stream, x, n, q, scale,
+                       partial + kMaxPartials, g_qz_spin_limit);
+    return hipGetLastError();
+  }
   if (vx && vq) {
     // With 64 floats per thread in registers, 4 workgroups per CU are resident (qz_cast
     // holds 110 VGPRs); 1024 workgroups cover 4096 x 4096 in one chunk each.
@@ -245,3 +378,8 @@ extern "C" hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* 
   hipLaunchKernelGGL(qz_cast_any, dim3(g2), dim3(kThreads), 0, stream, x, n, partial, g1, q, scale);
   return hipGetLastError();
 }
+
+// Test hook: the polls of the fused kernel's bounded wait before a workgroup falls back to
+// finding the max itself (0 sends every workgroup to the fallback).  Not thread-safe; for
+// tests that check both paths give the same bits.
+extern "C" void taskops_testing_quantize_spin_limit(unsigned polls) { g_qz_spin_limit = polls; }

@@ -44,7 +44,7 @@ DOMINANT = {
     "efficient_kan": "kan_gemm",
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny",
-    "quantize_e4m3": ("qz_amax", "qz_cast"),
+    "quantize_e4m3": "qz_fused",
 }
 COPY_PROBE_BYTES = 256 << 20
 

@@ -111,7 +111,9 @@ hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_
  * q[i] = e4m3(clamp(x[i] * *scale, -448, 448)), round to nearest even; a NaN in x makes
  * *scale and every q[i] NaN (0x7F or 0xFF: the sign of a computed NaN is unspecified).
  * q and scale are device pointers.  n == 0 writes nothing;
- * n < 0 returns hipErrorInvalidValue.
+ * n < 0 returns hipErrorInvalidValue.  Aligned x (16 B) and q (4 B) up to the resident
+ * capacity (1280 chunks of 16384 elements on an MI355X) take one launch with a bounded grid
+ * barrier; other calls take two launches.  Both give the same bits.
  * Replaces: tasks/fp8_linear/reference.py:15-18 (`_quantize`, which the reference runs on
  *           the CPU before the op). */
 hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* q, float* scale,

@@ -171,3 +171,56 @@ def test_gpu_quantize_back_to_back(lib):
         got = np.float32(s.item())
         assert (np.isnan(got) and np.isnan(s_want)) or got == s_want
         assert e4m3.same_codes(q.cpu().numpy(), q_want)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n", [1, 16385, 1 << 20])
+def test_gpu_quantize_fallback_path_same_bits(lib, n):
+    """The fused kernel's bounded wait, forced to time out at once (a test hook sets its poll
+    count to 0): every workgroup finds the max itself, and the bits equal the barrier path's
+    and the oracle's."""
+    import ctypes
+    print(f"\n[parity] quantize_e4m3 fallback n={n}", flush=True)
+    x = torch.randn(n, generator=torch.Generator().manual_seed(n + 3)) * 7.0
+    if n == 16385:
+        x[n // 3] = float("nan")                # a NaN carries through either path
+    q0, s0 = _run_gpu(lib, x)
+    hook = lib.taskops_testing_quantize_spin_limit
+    hook.argtypes = [ctypes.c_uint]
+    hook(0)
+    try:
+        q1, s1 = _run_gpu(lib, x)
+    finally:
+        hook(1 << 14)
+    q2, s2 = _run_gpu(lib, x)                 # and the barrier path again afterwards
+    q_want, s_want = e4m3.quantize(x.numpy())
+    for q, s in ((q0, s0), (q1, s1), (q2, s2)):
+        assert (np.isnan(s) and np.isnan(s_want)) or s == s_want
+        assert e4m3.same_codes(q, q_want)
+    assert np.array_equal(q0, q1) and np.array_equal(q0, q2)
+
+
+@pytest.mark.gpu
+def test_gpu_quantize_graph_replay(lib):
+    """Captured into a graph, the fused kernel's barrier state carries across replays (the
+    sense flips every launch)."""
+    n = 300_000
+    xd = torch.empty(n, device="cuda")
+    q = torch.empty(n, dtype=torch.uint8, device="cuda")
+    sd = torch.empty(1, device="cuda")
+    args = dict(x=xd, n=n, q=q, scale=sd)
+    xd.copy_(torch.randn(n, generator=torch.Generator().manual_seed(1)))
+    capi.call(lib, "quantize_e4m3", args)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        capi.call(lib, "quantize_e4m3", args)
+    for k in range(4):
+        x = torch.randn(n, generator=torch.Generator().manual_seed(10 + k)) * (k + 1)
+        xd.copy_(x)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        q_want, s_want = e4m3.quantize(x.numpy())
+        assert float(sd.item()) == float(s_want)
+        assert np.array_equal(q.cpu().numpy(), q_want)
