@@ -223,7 +223,7 @@ constexpr int kQzGroups = 16;
 constexpr int kQzLine = 16;  // unsigned per 64-byte line
 enum QzWord : int { kQzGroupCount = 0, kQzGroupMax = kQzGroups, kQzTopCount = 2 * kQzGroups, kQzTopMax,
                     kQzResult, kQzSense, kQzWords };
-constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the sense flag (~1 us each) before the fallback
+constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the sense flag (~0.5-1 us each) before the fallback
 
 __device__ __forceinline__ unsigned* qz_word(unsigned* bar, int w, int i = 0) { return bar + (w + i) * kQzLine; }
 __device__ __forceinline__ unsigned qz_load(unsigned* p) {
