@@ -203,7 +203,7 @@ def main() -> int:
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {a.gpus} is not supported (the six task ops "
-              "are single-GPU kernels; see DESIGN.md for how they would shard)", file=sys.stderr)
+              "are single-GPU kernels and this build has no multi-GPU path)", file=sys.stderr)
         return 2
 
     import torch
