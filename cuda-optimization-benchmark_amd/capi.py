@@ -106,6 +106,24 @@ def call(lib: ctypes.CDLL, op: str, args: dict, stream: int | None = None) -> No
         raise TaskOpsError(f"{sym} returned hipError_t {rc}")
 
 
+def bind(lib: ctypes.CDLL, op: str, args: dict, stream: int | None = None):
+    """`call` with the arguments converted once: returns a function of no arguments that
+    invokes the entry point and raises TaskOpsError on a non-zero hipError_t.  The tensors
+    in `args` must stay alive (and at the same addresses) while it is used."""
+    sym, params = ENTRY[op]
+    if stream is None:
+        stream = torch.cuda.current_stream().cuda_stream
+    cargs = tuple(ctypes.c_void_p(_ptr(args[name])) if ctype is _P else ctype(args[name])
+                  for name, ctype in params) + (ctypes.c_void_p(stream),)
+    fn = getattr(lib, sym)
+
+    def run() -> None:
+        rc = fn(*cargs)
+        if rc != 0:
+            raise TaskOpsError(f"{sym} returned hipError_t {rc}")
+    return run
+
+
 def output_shapes(op: str, inp: dict) -> dict:
     """Output name -> (shape, dtype) for the drop-in ops (from the task spec)."""
     task = load_task(op)

@@ -44,3 +44,22 @@ def test_dropin_exports(op):
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(capi.TaskOpsError):
         capi.load(tmp_path / "libtaskops.so")
+
+
+@pytest.mark.gpu
+def test_bound_call_matches_call():
+    """capi.bind (the bench's per-call path) passes the same arguments as capi.call."""
+    import torch
+    from cob_amd import inputs
+    print("\n[capi] bind vs call: reward_to_go", flush=True)
+    lib = capi.load()
+    case = dict(name="bind", seed=9, B=7, T=1100, gamma=0.97, done_p=0.05)
+    args = capi.device_args("reward_to_go", inputs.make_inputs("reward_to_go", case))
+    a = torch.empty(7 * 1100, device="cuda")
+    b = torch.full((7 * 1100,), float("nan"), device="cuda")
+    capi.call(lib, "reward_to_go", dict(args, output=a))
+    run = capi.bind(lib, "reward_to_go", dict(args, output=b))
+    run()
+    run()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
