@@ -1,0 +1,77 @@
+"""bench.py on the CPU: the algorithmic work each roofline divides by, derived here from the
+BASELINE shapes by the byte and FLOP counts of each op's interface (not copied from the
+table), the cache-cold rotation, and the refusals (more than one GPU, no GPU)."""
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+sys.path.insert(0, str(ROOT))
+import bench  # noqa: E402
+from cob_amd import tasks  # noqa: E402
+
+F32, BF16, BYTE = 4, 2, 1
+
+
+def _work(key):
+    """Bytes (HBM-bound) or FLOP (MFMA-bound) of one call at the BASELINE shape."""
+    c = tasks.BASELINE[bench.WORKLOADS[key][1]]
+    if key == "reward_to_go":                  # reward f32 + done bool in, f32 out
+        return c["B"] * c["T"] * (F32 + BYTE + F32)
+    if key == "pow_abs_sqrt_mean":             # two f32 inputs, one f32 scalar out
+        return 2 * F32 * c["batch_size"] * 4 * c["height"] * c["width"] + F32
+    if key == "leaky":                         # x in, spikes out per step; mem0 in, final out; beta, threshold
+        return (c["T"] * c["B"] * c["H"] * 2 * F32 + c["B"] * c["H"] * 2 * F32 + c["H"] * 2 * F32)
+    n = c.get("B", 0) * c.get("T", 0) * c.get("H", 0)
+    if key == "ppo_clip":                      # cur, old, adv, entropy in; 8 f32 out
+        return 4 * F32 * n + 8 * F32
+    if key == "ppo_clip_dropin":               # cur, old, adv in; 6 f32 out
+        return 3 * F32 * n + 6 * F32
+    if key == "efficient_kan":                 # one contraction over I*(1 + G + K) per output
+        return 2 * c["B"] * c["O"] * c["I"] * (1 + c["grid_size"] + c["spline_order"])
+    if key == "fp8_linear":
+        return 2 * c["M"] * c["N"] * c["K"]
+    if key == "fp8_linear_m16":                # w and x e4m3, bias bf16 in; bf16 out
+        return c["N"] * c["K"] * BYTE + c["M"] * c["K"] * BYTE + c["N"] * BF16 + c["M"] * c["N"] * BF16
+    if key == "quantize_e4m3":                 # fp32 x in, e4m3 codes out (the scale is 4 bytes)
+        return c["M"] * c["K"] * (F32 + BYTE)
+    raise KeyError(key)
+
+
+@pytest.mark.parametrize("key", bench.ORDER)
+def test_algorithmic_work(key):
+    assert bench.WORKLOADS[key][3] == _work(key)
+
+
+def test_every_workload_is_benched_and_bounded():
+    assert sorted(bench.ORDER) == sorted(bench.WORKLOADS)
+    for key, (entry, bkey, bound, _, dtype, _) in bench.WORKLOADS.items():
+        assert bkey in tasks.BASELINE and bound in ("hbm", "mfma")
+        if bound == "mfma":
+            assert dtype in bench.PEAK_TFLOPS
+
+
+def test_cold_rotation_exceeds_the_mall():
+    """Working sets under the 256 MiB MALL rotate through enough copies to exceed it twice."""
+    rtg = 4096 * 4096 * 9
+    assert bench._copies(rtg) == 4 and 4 * rtg >= 2 * bench.MALL_BYTES
+    assert bench._copies(2 * bench.MALL_BYTES) == 1
+    assert bench._copies(1) == 24
+
+
+def test_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_needs_a_gpu():
+    """Without a GPU bench.py exits non-zero and prints no result line (no CPU fallback)."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--no-cpu", "--ops", "reward_to_go"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 1 and "needs a GPU" in r.stderr and r.stdout == ""
