@@ -75,3 +75,28 @@ def test_needs_a_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--no-cpu", "--ops", "reward_to_go"],
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 1 and "needs a GPU" in r.stderr and r.stdout == ""
+
+
+@pytest.mark.gpu
+@pytest.mark.timeout(300)
+def test_json_line_on_gpu():
+    """One short bench.py run: a single JSON line with the contract's fields, the roofline of
+    the timed kernel and the CPU baseline."""
+    import json
+    print("\n[bench] reward_to_go --steps 5", flush=True)
+    r = subprocess.run([sys.executable, "-u", str(ROOT / "bench.py"), "--ops", "reward_to_go", "--steps", "5",
+                        "--warmup", "1"], capture_output=True, text=True, timeout=280)
+    assert r.returncode == 0, r.stderr[-3000:]
+    lines = [ln for ln in r.stdout.splitlines() if ln.strip()]
+    assert len(lines) == 1
+    d = json.loads(lines[0])
+    assert d["n_gpus"] == 1 and d["steps"] == 5 and d["warmup"] == 1 and d["unit"] == "us/call"
+    assert d["higher_is_better"] is False and d["vs_baseline"] is None and d["data"].startswith("synthetic")
+    assert d["value"] > 0 and abs(d["ms_per_step"] * 1e3 - d["value"]) < 1e-3 * d["value"] + 1e-3
+    assert "reward_to_go" in d["config"]["workload"]
+    roof = d["roofline"]
+    assert roof["bound"] == "hbm" and roof["peak"] == bench.HBM_PEAK_GBS and roof["unit"] == "GB/s"
+    assert abs(roof["achieved"] - _work("reward_to_go") / (d["value"] * 1e-6) / 1e9) < 0.01 * roof["achieved"]
+    assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
+    cpu = d["cpu_baseline"]
+    assert cpu["value"] > 0 and cpu["unit"] == "us/call" and cpu["cores"] >= 1 and cpu["kind"] == "port"
