@@ -149,7 +149,8 @@ enum WorkspaceSlot : int {
 };
 
 // Returns a zero-initialised device buffer of at least `bytes` for `slot` on the current
-// device, allocated on the first request.  A later request for more bytes allocates a
+// device, allocated on the first request; hipErrorInvalidValue when `stream` belongs to
+// another device.  A later request for more bytes allocates a
 // larger one (the old one is kept until the process exits, since kernels enqueued before
 // may still use it).  The zero fill is a kernel enqueued on `stream`, ordered before the
 // caller's launches.

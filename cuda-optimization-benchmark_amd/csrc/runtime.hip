@@ -35,6 +35,14 @@ hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void*
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
   if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  // The workspace is the current device's; kernels run on the stream's device.  A stream of
+  // another device is refused rather than handed memory it cannot use.
+  if (stream != nullptr) {
+    hipDevice_t sdev = 0;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return e;
+    if (sdev != dev) return hipErrorInvalidValue;
+  }
   std::lock_guard<std::mutex> lock(g_mu);
   Region& r = g_regions[dev][slot];
   if (r.bytes < bytes) {
