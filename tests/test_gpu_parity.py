@@ -52,7 +52,9 @@ def test_baseline_reward_to_go(lib):
     inp = _baseline("reward_to_go")
     got = capi.run_op(lib, "reward_to_go", inp)["output"]
     s = compare(got.cpu(), exact.reward_to_go(inp)["output"], tasks.load_task("reward_to_go")["tolerance"])
-    assert s["bad"] == 0, s
+    print(f"[parity] worst error {s['worst']:.4f} of the tolerance", flush=True)
+    # fp64 carries and fp32 lane-local steps: a margin, not just a pass.
+    assert s["bad"] == 0 and s["worst"] < 0.25, s
 
 
 def test_baseline_leaky_bit_exact(lib):
