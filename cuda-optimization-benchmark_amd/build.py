@@ -76,11 +76,11 @@ def _compile(src: str) -> Path:
 
 
 def dropin_source(op: str) -> str:
-    """The grader shim for one op, generated from the task's signature the way
-    graders/grade.py:85-89 generates it, with dropin.hpp standing in for solution.cu."""
-    from .grader.shim import parse_signature, shim_source
+    """The grader shim for one op (the calling convention of graders/grade.py:85-89),
+    generated from the task's HIP signature, with dropin.hpp standing in for solution.cu."""
+    from .grader.signature import parse, shim
     from .tasks import load_task
-    return shim_source(parse_signature(load_task(op)["hip_signature"]))
+    return shim(parse(load_task(op)["hip_signature"]))
 
 
 def build(verbose: bool = True, jobs: int | None = None) -> Path:

@@ -153,13 +153,14 @@ def hip_signature(sig: str) -> str:
 
 
 def load_task(op: str) -> dict:
-    """The task record of one op, shaped like graders/grade.py:66-70 returns it."""
-    from .grader.shim import parse_signature
+    """The task record of one op: its signature (and the parsed parameters), outputs,
+    tolerance and cases."""
+    from .grader.signature import parse
     t = {"task": op, "signature": _SIG[op], "outputs": copy.deepcopy(_OUT[op]),
          "tolerance": dict(_TOL[op]), "cases": copy.deepcopy(_HIDDEN[op]),
          "public_cases": copy.deepcopy(_PUBLIC[op])}
     t["hip_signature"] = hip_signature(t["signature"])
-    t["params"] = parse_signature(t["signature"])
+    t["params"] = parse(t["signature"])
     return t
 
 

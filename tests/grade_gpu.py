@@ -1,16 +1,16 @@
-"""Grade the six drop-in kernels the way the reference's grader does, on one GPU, and write
-one log per kernel plus the tables (graders/grade.py + child.py; tables by
-cuda-optimization-benchmark_amd/grader/report.py).  Not collected by pytest; run as
+"""Grade the six drop-in kernels on one GPU and write one log per kernel plus the tables
+(the role of graders/grade.py + child.py; logs and tables by grader/ledger.py).  Not
+collected by pytest; run as
 
-    python tests/grade_gpu.py OUT_DIR [--ops a,b] [--passes 2]
+    python tests/grade_gpu.py OUT_DIR [--ops a,b] [--passes 2] [--no-timing]
 
 For each op (grade_op()): every hidden and public case through the three-call protocol on
-guarded buffers (grader/harness.py check()), in `--passes` passes, with the HIP call counter
-armed around each call; then the task's timed case in 3 interleaved rounds of the kernel
-and PyTorch eager on the GPU (harness.timing()).  tests/test_proof_flow.py runs grade_op()
-on the CPU with planted kernels.  The checker is oracle/exact.py and the eager
-side oracle/eager.py, which is why this driver lives under tests/.  There is no expert
-kernel on this GPU, so `% of expert speed` stays empty.
+a device arena (grader/protocol.py run_case), in `--passes` passes, with the HIP call
+counter armed around each call; then the task's timed case, kernel against PyTorch eager
+on the same GPU in alternating rounds (protocol.time_case).  tests/test_proof_flow.py
+runs grade_op() on the CPU with planted runners.  The checker is oracle/exact.py and the
+eager side oracle/eager.py, which is why this driver lives under tests/.  No expert
+(reference CUDA) kernel runs on this GPU, so "% of expert" stays empty.
 """
 import argparse
 import json
@@ -27,29 +27,29 @@ __graft_entry__.load_package()
 from cob_amd import callcount  # noqa: E402
 
 
-def grade_op(op, kernel, exact_fn, passes=2, counter=None, device="cuda", torch_ref=None, key=None, env=None,
+def grade_op(op, runner, checker, passes=2, hip_calls=None, device="cuda", eager=None, key=None, env=None,
              log=print):
-    """One kernel's grading log: every hidden and public case of `op` through check() in
-    `passes` passes, then (with `torch_ref`) the timed case's timing, and the verdict."""
+    """One kernel's log: every hidden and public case of `op` in `passes` passes, then
+    (with `eager`) the timed case's timing, and the verdict row."""
     from cob_amd import tasks
-    from cob_amd.grader import harness, report
+    from cob_amd.grader import ledger
+    from cob_amd.grader.protocol import run_case, time_case
     t0 = time.time()
-    out = {"key": key or f"taskops_{op}", "task": op, "env": env or {}, "compile": {"ok": True}, "passes": []}
+    entry = {"kernel": key or f"taskops_{op}", "task": op, "env": env or {}, "build": {"ok": True},
+             "passes": []}
     for p in range(passes):
-        cases = []
+        reports = []
         for case in tasks.all_cases(op):
             log(f"[grade] {op} pass {p + 1} {case['name']}")
-            rec = harness.check(op, case, exact_fn, kernel=kernel, device=device, counter=counter)
-            rec["name"] = case["name"]
-            cases.append(rec)
-        out["passes"].append({"cases": cases})
-    if torch_ref is not None:
+            reports.append(run_case(op, case, checker, runner=runner, device=device, hip_calls=hip_calls))
+        entry["passes"].append(reports)
+    if eager is not None:
         timed = next(c for c in tasks.all_cases(op) if c.get("timed"))
         log(f"[grade] {op} timing {timed['name']}")
-        out["timing"] = harness.timing(op, timed, torch_ref=torch_ref, kernel=kernel)
-    out["seconds"] = round(time.time() - t0, 2)
-    out["verdict"] = report.kernel_verdict(out)
-    return out
+        entry["timing"] = time_case(op, timed, eager=eager, runner=runner)
+    entry["wall_s"] = round(time.time() - t0, 2)
+    entry["verdict"] = ledger.verdict_row(entry)
+    return entry
 
 
 def main(argv=None) -> int:
@@ -63,7 +63,8 @@ def main(argv=None) -> int:
 
     import torch
     from cob_amd import LIB_DIR, tasks
-    from cob_amd.grader import harness, report
+    from cob_amd.grader import ledger
+    from cob_amd.grader.entry import DropInLibrary
     from oracle import eager, exact
     if not torch.cuda.is_available():
         print("grade_gpu.py needs a GPU", file=sys.stderr)
@@ -78,20 +79,20 @@ def main(argv=None) -> int:
     for op in ops:
         lib = LIB_DIR / f"dropin_{op}.so"
         if lib.exists():
-            log = grade_op(op, harness.DropIn(op), exact.reference_exact, passes=a.passes,
-                           counter=lambda fn: counter.count(fn, 0),
-                           torch_ref=None if a.no_timing else eager.reference, env=env,
-                           log=lambda m: print(m, file=sys.stderr, flush=True))
-            log["compile"] = {"ok": True, "lib": lib.name, "log_tail": ""}
+            entry = grade_op(op, DropInLibrary(op), exact.reference_exact, passes=a.passes,
+                             hip_calls=lambda fire: counter.count(fire, 0),
+                             eager=None if a.no_timing else eager.reference, env=env,
+                             log=lambda m: print(m, file=sys.stderr, flush=True))
+            entry["build"] = {"ok": True, "lib": lib.name, "tail": ""}
         else:
-            log = {"key": f"taskops_{op}", "task": op, "env": env,
-                   "compile": {"ok": False, "lib": lib.name, "log_tail": f"{lib} not built"}}
-            log["verdict"] = report.kernel_verdict(log)
-        (out / f"{log['key']}.json").write_text(json.dumps(log, indent=1))
-        v = log["verdict"]
+            entry = {"kernel": f"taskops_{op}", "task": op, "env": env, "passes": [],
+                     "build": {"ok": False, "lib": lib.name, "tail": f"{lib} not built"}}
+            entry["verdict"] = ledger.verdict_row(entry)
+        (out / f"{entry['kernel']}.json").write_text(json.dumps(entry, indent=1))
+        v = entry["verdict"]
         print(f"[grade] {op}: {v['status']} {v['label'] or ''} kernel {v['kernel_ms']} ms, "
-              f"x{v['speedup_vs_torch']} vs torch", file=sys.stderr, flush=True)
-    report.write_tables(out)
+              f"x{v['x_eager']} vs eager", file=sys.stderr, flush=True)
+    ledger.tables(out)
     print((out / "table.md").read_text(), end="")
     return 0
 

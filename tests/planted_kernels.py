@@ -1,18 +1,26 @@
-"""Planted CPU kernels for the negative controls (tests/test_planted.py, tests/test_proof_flow.py):
-a CPU kernel with the drop-in's bind/call interface that reads its inputs from the guarded
-input buffers it is handed, computes the op with the oracle and writes the guarded output
-buffers, except for one planted fault (graders/planted.py:10-53 plants the same faults in
-CUDA).  Not collected by pytest."""
+"""Planted runners for the negative controls: each has the grader's runner interface
+(`bind(arena, scalars) -> fire()`) and is wrong in one known way, so the harness must
+give it one known label (graders/planted.py:10-53 names the same kinds of fault).
+Not collected by pytest.
+
+- OracleKernel (CPU): reads its inputs from a host arena, computes the outputs with the
+  oracle, writes them, then plants its fault in host memory.  Used by the CPU tests.
+- DeviceFault (GPU): runs the real HIP kernel through its drop-in library on a device
+  arena, then plants its fault in device memory with torch's own device operations (a
+  fill, a copy, an add), so the harness's device-side checks -- guard gaps, 0xFF
+  outputs, unchanged inputs, call-2 results, repeat bits -- must catch it.  Every planted
+  write lands inside the arena's one allocation; no GPU kernel is altered.
+"""
 import numpy as np
 import torch
 
 from cob_amd import tasks
-from cob_amd.grader import harness
+from cob_amd.grader.arena import POISON_FILL
 from oracle import exact
 
 WRONG = 12345.0  # far from every op's results
 
-# plant -> (status, label) the verdict must give
+# planted fault -> (status, label) the verdict must give
 EXPECT = {
     None: ("pass", None),
     "wrong_value": ("fail", "wrong value"),
@@ -25,50 +33,101 @@ EXPECT = {
 }
 
 
-class PlantedCpuKernel:
-    """A CPU kernel behind DropIn's interface; `fault` names the planted mistake."""
+def _first_input(task):
+    return next(p.name for p in task["params"] if p.pointer and p.name not in task["outputs"])
+
+
+def _last_output(task):
+    return [p.name for p in task["params"] if p.name in task["outputs"]][-1]
+
+
+class _PerArena:
+    """Calls made into each arena (one arena per graded case), and what a caching plant
+    kept from the arena's first call."""
+
+    def __init__(self):
+        self.seen = {}
+
+    def next_call(self, arena):
+        entry = self.seen.setdefault(id(arena), [arena, 0, {}])   # the arena is kept alive
+        entry[1] += 1
+        return entry[1], entry[2]
+
+
+def _plant_after(fault, arena, task, calls, cache):
+    """Plant `fault` into the arena after the (correct) outputs have been written;
+    `calls` counts the calls into this arena, `cache` is its own."""
+    outs = arena.outputs()
+    if fault == "cached_result":
+        if calls == 1:
+            cache.update({n: arena.view(n).clone() for n in outs})
+        else:
+            for n in outs:
+                arena.view(n).copy_(cache[n])            # the first call's result, again
+    elif fault == "wrong_value":
+        arena.view(outs[0]).view(-1)[0] = WRONG
+    elif fault == "oob_write_before":
+        r = arena.by_name[outs[0]]
+        arena.mem[r.start - 1] = 0
+    elif fault == "oob_write_after":
+        r = arena.by_name[_last_output(task)]
+        arena.mem[r.start + r.nbytes] = 0
+    elif fault == "unwritten_output":
+        r = arena.by_name[_last_output(task)]
+        es = arena.view(r.name).element_size()
+        arena.mem[r.start + r.nbytes - es:r.start + r.nbytes] = POISON_FILL
+    elif fault == "input_modified":
+        r = arena.by_name[_first_input(task)]
+        arena.mem[r.start] ^= 0x01
+    elif fault == "nonrepeatable" and calls == 3:
+        # call 3 repeats call 1's inputs; one output differs in its lowest bit
+        flat = arena.view(outs[0]).view(-1)
+        flat.view(torch.int16 if flat.element_size() == 2 else torch.int32)[0] ^= 1
+
+
+class OracleKernel:
+    """A CPU runner: the oracle's outputs, written into a host arena, then `fault`."""
 
     def __init__(self, op: str, fault: str | None = None):
         self.op, self.fault = op, fault
         self.task = tasks.load_task(op)
-        self.calls = 0
+        self.arenas = _PerArena()
 
-    def bind(self, bufs: dict, scalars: dict):
-        return (bufs, scalars), None
-
-    def _inputs(self, bufs, scalars) -> dict:
-        inp = dict(scalars)
-        for ctype, name in self.task["params"]:
-            if "*" in ctype and name not in self.task["outputs"]:
-                t = bufs[name].t.clone()
-                inp[name] = t.view(torch.float8_e4m3fn) if "fp8" in ctype else t
-        return inp
-
-    def __call__(self, arr) -> None:
-        bufs, scalars = arr
-        self.calls += 1
-        if self.fault == "cached_result" and self.calls > 1:
-            return  # assumes the inputs never change between calls
-        want = exact.reference_exact(self.op, self._inputs(bufs, scalars))
-        for name in self.task["outputs"]:
-            out = bufs[name].t
-            flat = out.view(-1)
-            flat.copy_(torch.as_tensor(np.asarray(want[name], dtype=np.float64)).reshape(-1).to(out.dtype))
-            g = harness.GUARD
-            if self.fault == "wrong_value":
-                flat[0] = WRONG
-            elif self.fault == "oob_write_before":
-                bufs[name].raw[g - 1] = 0
-            elif self.fault == "oob_write_after":
-                bufs[name].raw[g + bufs[name].n] = 0
-            elif self.fault == "unwritten_output":
-                es = flat.element_size()
-                bufs[name].raw[g + bufs[name].n - es:g + bufs[name].n] = harness.POISON
-            elif self.fault == "nonrepeatable" and self.calls == 3:
-                # call 3 repeats call 1's inputs; one output differs by one unit in the last place
-                flat.view(torch.int16 if flat.element_size() == 2 else torch.int32)[0] ^= 1
-        if self.fault == "input_modified":
-            name = next(n for c, n in self.task["params"] if "*" in c and n not in self.task["outputs"])
-            bufs[name].raw[harness.GUARD] ^= 0x01
+    def bind(self, arena, scalars):
+        def fire():
+            calls, cache = self.arenas.next_call(arena)
+            if not (self.fault == "cached_result" and calls > 1):
+                inp = dict(scalars)
+                for p in self.task["params"]:
+                    if p.pointer and p.name not in self.task["outputs"]:
+                        t = arena.view(p.name).clone()
+                        inp[p.name] = t.view(torch.float8_e4m3fn) if "fp8" in p.ctype else t
+                want = exact.reference_exact(self.op, inp)
+                for name in arena.outputs():
+                    out = arena.view(name)
+                    vals = torch.as_tensor(np.asarray(want[name], dtype=np.float64)).reshape(out.shape)
+                    out.copy_(vals.to(out.dtype))
+            _plant_after(self.fault, arena, self.task, calls, cache)
+        return fire
 
 
+class DeviceFault:
+    """A GPU runner: the op's real drop-in kernel on a device arena, then `fault` planted
+    in device memory by a torch device operation."""
+
+    def __init__(self, op: str, fault: str | None = None):
+        from cob_amd.grader.entry import DropInLibrary
+        self.op, self.fault = op, fault
+        self.task = tasks.load_task(op)
+        self.lib = DropInLibrary(op)
+        self.arenas = _PerArena()
+
+    def bind(self, arena, scalars):
+        kernel = self.lib.bind(arena, scalars)
+
+        def fire():
+            calls, cache = self.arenas.next_call(arena)
+            if not (self.fault == "cached_result" and calls > 1):
+                kernel()
+            _plant_after(self.fault, arena, self.task, calls, cache)
+        return fire

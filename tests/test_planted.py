@@ -1,66 +1,59 @@
-"""Planted negative controls: kernels that are wrong in one known way must draw their named
-label from the same harness the real kernels are graded by (the three-call protocol on
-guarded buffers, grader/harness.py check(); labels, grader/verdict.py).  Counterpart of
-graders/planted.py:10-53 (EXPECT) with the labels of graders/verdict.py:35-61.
+"""Planted negative controls on the CPU: a runner that is wrong in one known way must draw
+its named label from the same protocol, arena and label rules the HIP kernels are graded
+by (grader/protocol.py, grader/labels.py).  The counterpart of graders/planted.py:10-53.
 
-The plants run on the CPU, never as GPU code.  Each is a CPU kernel with the drop-in's
-bind/call interface: it reads its inputs from the guarded input buffers it is handed,
-computes the op with the oracle and writes the guarded output buffers, except for one
-planted fault.  The buffers live in host memory (check(device="cpu")); everything else is
-the harness the GPU tests use.
+Here the runners are tests/planted_kernels.py's OracleKernel: the oracle's outputs
+written into a host arena, with one fault planted afterwards.  tests/test_planted_device.py
+plants the same faults in device memory around the real HIP kernels.
 
 The reference's race and uninitialised-read plants have no counterpart: they are caught by
-compute-sanitizer's racecheck and initcheck, and ROCm has neither.  Races are covered by
-design review and the bitwise repeat check (the `nonrepeatable` plant shows that check
-firing); unwritten outputs by the 0xFF poison (`unwritten_output`).
+compute-sanitizer's racecheck and initcheck, which ROCm lacks.  Races are covered by design
+review and the bitwise repeat check (the `nonrepeatable` plant shows it firing), and
+unwritten outputs by the 0xFF fill (`unwritten_output`).
 """
 import pytest
 
 from cob_amd import tasks
-from cob_amd.grader import harness
-from cob_amd.grader.verdict import case_result, verdict
+from cob_amd.grader.labels import case_outcome, kernel_status
+from cob_amd.grader.protocol import run_case
 from oracle import exact
-from planted_kernels import EXPECT, PlantedCpuKernel
+from planted_kernels import EXPECT, OracleKernel
 
 
-def _case(op):
+def _public(op):
     return next(c for c in tasks.all_cases(op) if c["name"].startswith("public_"))
+
+
+def _grade(op, fault):
+    return run_case(op, _public(op), exact.reference_exact, runner=OracleKernel(op, fault), device="cpu")
 
 
 @pytest.mark.parametrize("fault", list(EXPECT))
 @pytest.mark.parametrize("op", tasks.OPS)
 def test_planted_control_gets_its_label(op, fault):
-    case = _case(op)
-    rec = harness.check(op, case, exact.reference_exact, kernel=PlantedCpuKernel(op, fault), device="cpu")
-    rec["name"] = case["name"]
-    v = verdict([[rec]])
-    assert (v["status"], v["label"]) == EXPECT[fault], (rec.get("compare"), rec["calls"])
-    if fault in (None, "wrong_value", "oob_write_before", "oob_write_after", "input_modified"):
-        assert v["identical_repeat"] is True
-    if fault == "nonrepeatable":
-        assert v["identical_repeat"] is False
+    report = _grade(op, fault)
+    st = kernel_status([[report]])
+    assert (st["status"], st["label"]) == EXPECT[fault], (report["checks"], report["calls"])
+    assert st["repeat_identical"] is (fault != "nonrepeatable")
 
 
 @pytest.mark.parametrize("op", ["reward_to_go", "fp8_linear"])
-def test_planted_flip_between_passes(op):
-    """A kernel right in one pass and wrong in the other is a flip, labelled by its failure."""
-    case = _case(op)
-    passes = []
-    for fault in (None, "wrong_value"):
-        rec = harness.check(op, case, exact.reference_exact, kernel=PlantedCpuKernel(op, fault), device="cpu")
-        rec["name"] = case["name"]
-        passes.append([rec])
-    v = verdict(passes)
-    assert (v["status"], v["label"]) == ("flip", "wrong value")
-    assert v["passes"] == ["pass", "fail"]
+def test_right_then_wrong_is_a_flip(op):
+    passes = [[_grade(op, None)], [_grade(op, "wrong_value")]]
+    st = kernel_status(passes)
+    assert (st["status"], st["label"], st["passes"]) == ("flip", "wrong value", ["pass", "fail"])
 
 
-def test_planted_failure_names_the_check():
-    """The failing check names the call and buffer, as the reference's logs do."""
+def test_failure_names_the_call_and_region():
+    """The location names the call, the region and the first byte that moved."""
     op = "leaky"
-    case = _case(op)
-    rec = harness.check(op, case, exact.reference_exact, kernel=PlantedCpuKernel(op, "oob_write_after"), device="cpu")
-    ok, chk, label = case_result(rec)
-    assert (ok, chk, label) == (False, "call1:guards", "out-of-bounds write")
-    rec = harness.check(op, case, exact.reference_exact, kernel=PlantedCpuKernel(op, "cached_result"), device="cpu")
-    assert case_result(rec)[1].startswith("call2:")
+    o = case_outcome(_grade(op, "oob_write_after"))
+    assert o["label"] == "out-of-bounds write" and o["where"].startswith("call 1: gap after final_mem (byte ")
+    o = case_outcome(_grade(op, "oob_write_before"))
+    assert o["where"].startswith("call 1: gap before spikes")
+    o = case_outcome(_grade(op, "input_modified"))
+    assert o["where"].startswith("call 1: input input_current")
+    o = case_outcome(_grade(op, "cached_result"))
+    assert (o["label"], o["where"]) == ("stale state", "call 2: spikes")
+    o = case_outcome(_grade(op, "unwritten_output"))
+    assert (o["label"], o["where"]) == ("unwritten output", "call 1: final_mem")

@@ -1,33 +1,34 @@
-"""The grading flow end to end on the CPU (graders/tests/test_grade.py:187-219 runs the
-reference's `proof` flow with a fake GPU process): tests/grade_gpu.py's grade_op() writes
-per-kernel logs for a correct CPU kernel and for each planted one, and grader/report.py
-turns the logs into the verdict table — the correct kernel passes, each plant carries its
-label, and regrading the stored logs reproduces the table."""
+"""The grading flow end to end on the CPU: tests/grade_gpu.py's grade_op() writes one log
+per runner -- a correct one and each planted one (tests/planted_kernels.py OracleKernel)
+-- and grader/ledger.py turns the logs into the verdict table: the correct runner passes,
+each plant carries its label, and regrading the stored logs gives the same table."""
 import json
 
 import pytest
 
-from cob_amd.grader import report
+from cob_amd.grader import ledger
 from oracle import exact
-from planted_kernels import EXPECT, PlantedCpuKernel
+from planted_kernels import EXPECT, OracleKernel
 from grade_gpu import grade_op
+
+
+def _key(fault, op):
+    return f"{'correct' if fault is None else 'planted_' + fault}__{op}"
 
 
 @pytest.mark.parametrize("op", ["reward_to_go", "ppo_clip"])
 def test_proof_flow_on_cpu(tmp_path, op):
-    quiet = lambda m: None  # noqa: E731
     for fault in EXPECT:
-        key = f"{'expert' if fault is None else 'planted_' + fault}__{op}"
-        log = grade_op(op, PlantedCpuKernel(op, fault), exact.reference_exact, passes=1, device="cpu", key=key,
-                       log=quiet)
-        (tmp_path / f"{key}.json").write_text(json.dumps(log))
-    rows = {r["key"]: r for r in report.write_tables(tmp_path)}
+        entry = grade_op(op, OracleKernel(op, fault), exact.reference_exact, passes=1, device="cpu",
+                         key=_key(fault, op), log=lambda m: None)
+        (tmp_path / f"{entry['kernel']}.json").write_text(json.dumps(entry))
+    rows = {r["kernel"]: r for r in ledger.tables(tmp_path)}
     assert len(rows) == len(EXPECT)
     for fault, (status, label) in EXPECT.items():
-        r = rows[f"{'expert' if fault is None else 'planted_' + fault}__{op}"]
+        r = rows[_key(fault, op)]
         assert (r["status"], r["label"]) == (status, label), r
-    assert rows[f"planted_nonrepeatable__{op}"]["identical_repeat"] is False
+    assert rows[_key("nonrepeatable", op)]["repeat_identical"] is False
     table = (tmp_path / "table.md").read_text()
-    assert (tmp_path / "table.md").read_text().count("\n") == len(EXPECT) + 2
-    report.regrade(tmp_path)
+    assert table.count("\n") == len(EXPECT) + 2
+    ledger.tables(tmp_path, recompute=True)
     assert (tmp_path / "table.md").read_text() == table
