@@ -231,7 +231,7 @@ def test_baseline_repeat_bits(lib, op, key, entropy):
     seen = []
     for _ in range(2):
         for o in outs.values():
-            o.view(torch.uint8).fill_(0xFF)
+            o.reshape(-1).view(torch.uint8).fill_(0xFF)
         capi.call(lib, entry, dict(args, **outs))
         torch.cuda.synchronize()
         seen.append({n: o.clone() for n, o in outs.items()})
