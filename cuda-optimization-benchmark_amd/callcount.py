@@ -86,6 +86,7 @@ def load_counter(path: str | Path | None = None) -> Counter:
 # Launches per steady call of each entry point and path.
 EXPECTED_LAUNCHES = {
     "pow_abs_sqrt_mean": 1, "leaky": 1, "reward_to_go": 1, "ppo_clip": 1, "ppo_clip_entropy": 1,
+    "ppo_clip_entropy_noalloc": 1,  # its first call on a device adds the scratch clear
     "efficient_kan": 3,          # kan_prepare + kan_pack + kan_gemm (spline order 3)
     "efficient_kan_rowwise": 1,  # kan_rowwise (other spline orders)
     "fp8_linear": 1,
@@ -96,8 +97,8 @@ EXPECTED_LAUNCHES = {
 
 def workloads():
     """(name, entry point, expectation key, make_args) for every hidden and public case of
-    the six ops, the entropy variant of ppo_clip, the row-wise efficient_kan path and the
-    quantiser (aligned and unaligned)."""
+    the six ops, the entropy variant of ppo_clip (allocating and not), the row-wise
+    efficient_kan path and the quantiser (aligned and unaligned)."""
     import torch
     from cob_amd import capi, inputs, tasks
 
@@ -136,6 +137,8 @@ def workloads():
             if op == "ppo_clip":
                 out.append((f"ppo_clip_entropy/{case['name']}", "ppo_clip_entropy", "ppo_clip_entropy",
                             drop_in(op, case, entropy=True)))
+                out.append((f"ppo_clip_entropy_noalloc/{case['name']}", "ppo_clip_entropy_noalloc",
+                            "ppo_clip_entropy_noalloc", drop_in(op, case, entropy=True)))
     for order in (1, 2):
         case = dict(name=f"B64_I40_O24_order{order}", seed=70 + order, small=True, timed=False,
                     B=64, I=40, O=24, spline_order=order)

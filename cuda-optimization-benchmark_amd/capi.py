@@ -41,6 +41,11 @@ ENTRY = {
                          [("B", _I32), ("T", _I32), ("H", _I32), ("current_log_prob", _P),
                           ("old_log_prob", _P), ("advantage", _P), ("entropy", _P),
                           ("clip_epsilon", _F32), ("entropy_coef", _F32), ("output", _P)]),
+    # ppo_clip_entropy with its scratch in a fixed device array: no allocation at all.
+    "ppo_clip_entropy_noalloc": ("taskops_ppo_clip_entropy_noalloc",
+                                 [("B", _I32), ("T", _I32), ("H", _I32), ("current_log_prob", _P),
+                                  ("old_log_prob", _P), ("advantage", _P), ("entropy", _P),
+                                  ("clip_epsilon", _F32), ("entropy_coef", _F32), ("output", _P)]),
     "efficient_kan": ("taskops_efficient_kan",
                       [("x", _P), ("grid", _P), ("base_weight", _P), ("spline_weight", _P),
                        ("spline_scaler", _P), ("grid_size", _I32), ("spline_order", _I32),

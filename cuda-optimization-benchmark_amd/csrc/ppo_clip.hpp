@@ -79,7 +79,7 @@ template <int kThreads, int kUnroll, bool kVec, bool kEntropy, bool kNT>
 __global__ __launch_bounds__(kThreads) void ppo_clip_kernel(
     int64_t n, const float* __restrict__ cur, const float* __restrict__ old,
     const float* __restrict__ adv, const float* __restrict__ ent, PpoParams p, float coef,
-    PpoWorkspace* __restrict__ ws, float* __restrict__ out) {
+    double (*__restrict__ records)[8], Arrivals* __restrict__ arrivals, float* __restrict__ out) {
   using namespace ppo_detail;
   constexpr int kFields = kPpoFields;
   __shared__ double lds[kFields][kThreads / kWave];
@@ -162,14 +162,14 @@ __global__ __launch_bounds__(kThreads) void ppo_clip_kernel(
       t = (f == kFields - 1) ? fmax(t, lds[f][w]) : t + lds[f][w];
     rec[f] = t;
   }
-  if (!publish_and_arrive<kFields>(ws->partial[blockIdx.x], rec, &ws->arrivals, &last)) return;
+  if (!publish_and_arrive<kFields>(records[blockIdx.x], rec, arrivals, &last)) return;
 
   // Finishing workgroup: wave w reduces fields w, w + waves, ... over all records (ratios
   // are positive, so 0 is the identity of the max as well as of the sums).
   __syncthreads();
   for (int f = wave; f < kFields; f += kThreads / kWave) {
-    double t = (f == kFields - 1) ? gather_records<true>(&ws->partial[0][f], 8, (int)gridDim.x, lane, kWave)
-                                  : gather_records<false>(&ws->partial[0][f], 8, (int)gridDim.x, lane, kWave);
+    double t = (f == kFields - 1) ? gather_records<true>(&records[0][f], 8, (int)gridDim.x, lane, kWave)
+                                  : gather_records<false>(&records[0][f], 8, (int)gridDim.x, lane, kWave);
     if (f == kFields - 1) {
 #pragma unroll
       for (int off = kWave / 2; off > 0; off >>= 1) t = fmax(t, __shfl_xor(t, off, kWave));

@@ -69,6 +69,7 @@ hipError_t taskops_reward_to_go(const float* reward, const bool* done, float gam
 
 /* PPO clipped objective and metrics over N = B*T*H samples, one pass, one launch.
  * output[0..5] = [loss_objective, clip_fraction, approx_kl, ess, max_ratio, mean_ratio].
+ * B, T or H <= 0, or B*T*H above 2^40, returns hipErrorInvalidValue and writes nothing.
  * Replaces: reference/ppo_clip/solution.cu:165-182 (tasks/ppo_clip/tests/task.json:3;
  *           op: tasks/ppo_clip/reference.py:27-39). */
 hipError_t taskops_ppo_clip(int32_t B, int32_t T, int32_t H, const float* current_log_prob,
@@ -85,6 +86,22 @@ hipError_t taskops_ppo_clip_entropy(int32_t B, int32_t T, int32_t H,
                                     const float* advantage, const float* entropy,
                                     float clip_epsilon, float entropy_coef, float* output,
                                     hipStream_t stream);
+
+/* taskops_ppo_clip_entropy without any allocation: the same kernel, launch shape and result
+ * bits, with the reduction's scratch (per-workgroup records and arrival counters) in a
+ * fixed 263,232-byte device array of the library instead of a workspace allocated on the
+ * first call.  No counterpart in the reference: it is for callers that cannot call
+ * hipMalloc (code under HIP graph capture, serving loops, harnesses that forbid it).
+ * Every call on one GPU shares that GPU's array, so calls that overlap in time on one GPU
+ * (different streams, or host threads) race; calls on one stream are safe.  The first call
+ * on a device clears the array with a kernel on `stream`.  Any B*T*H up to 2^40 samples
+ * fits; larger products and B, T or H <= 0 return hipErrorInvalidValue and write nothing. */
+hipError_t taskops_ppo_clip_entropy_noalloc(int32_t B, int32_t T, int32_t H,
+                                            const float* current_log_prob,
+                                            const float* old_log_prob, const float* advantage,
+                                            const float* entropy, float clip_epsilon,
+                                            float entropy_coef, float* output,
+                                            hipStream_t stream);
 
 /* KANLinear forward: out[B,O] = silu(x) @ base_weight^T
  *                              + bsplines(x; grid) @ (spline_weight * spline_scaler[...,None])^T
