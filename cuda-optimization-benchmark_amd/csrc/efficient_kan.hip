@@ -2,17 +2,15 @@
 //
 // Drop-in signature tasks/efficient_kan/tests/task.json:3, replacing
 // reference/efficient_kan/solution.cu:177-288.  Fast path (efficient_kan.hpp): spline
-// order 3 with at most 16 knots per feature — one launch that prepares the weights and
-// basis tables, and one fused fp16x3 MFMA GEMM.  Other shapes take the row-wise fp32 path
-// below.
+// order 3 with at most 16 knots per feature — kan_prepare (column scales), kan_pack (the
+// scaled fp16 hi/lo weights in the GEMM's K order, basis tables) and the warp-specialized
+// fp16x3 MFMA GEMM kan_fused.  Other shapes take the row-wise fp32 path below.
 #include <algorithm>
 
 #include "efficient_kan.hpp"
 
 namespace taskops {
 namespace {
-
-constexpr int kStages = 4;  // weight ring depth of kan_gemm
 
 // Row-wise fp32 path for shapes outside the fast path: the expanded activation row is
 // built in LDS with the Cox-de Boor recurrence, one output column per thread.
@@ -70,7 +68,7 @@ bool fast_path_fits(int B, int I, int O, int Cp) {
   const size_t ngroups = (I + kGroup - 1) / kGroup, Opad = ((O + BN - 1) / BN) * (size_t)BN;
   const size_t lim = 0x7fffffffu;
   return (size_t)B * I * 4 < lim && (size_t)B * O * 4 < lim &&
-         ngroups * (1 + Cp) * Opad * kChunk * 2 + (size_t)Opad * kChunk * 2 * kStages < lim;
+         ngroups * (1 + Cp) * Opad * kChunk * 2 < lim;
 }
 
 template <int kCp>
@@ -117,17 +115,16 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
                      ws, sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const size_t lds = (size_t)kStages * kStageBytes + kTblBytes;
   const bool vec = (O % 4) == 0 && (I % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(x) & 15) == 0;
   if (vec)
-    hipLaunchKernelGGL((kan_gemm<kCp, true>), dim3(tiles * nsplit), dim3(kThreads), lds, stream, x, tables, uflags,
-                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper, partial,
-                       counters);
+    hipLaunchKernelGGL((kan_fused<kCp, true>), dim3(tiles * nsplit), dim3(kThreads), kLdsBytes, stream, x, tables,
+                       uflags, table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper,
+                       partial, counters);
   else
-    hipLaunchKernelGGL((kan_gemm<kCp, false>), dim3(tiles * nsplit), dim3(kThreads), lds, stream, x, tables, uflags,
-                       table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper, partial,
-                       counters);
+    hipLaunchKernelGGL((kan_fused<kCp, false>), dim3(tiles * nsplit), dim3(kThreads), kLdsBytes, stream, x, tables,
+                       uflags, table_blocks, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit, gper,
+                       partial, counters);
   return hipGetLastError();
 }
 

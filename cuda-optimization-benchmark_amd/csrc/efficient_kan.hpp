@@ -4,10 +4,10 @@
 //   out[b,o] = sum_i silu(x[b,i]) Wb[o,i] + sum_i sum_c B_c(x[b,i]) Ws[o,i,c] sc[o,i]
 // with B_c the order-p B-spline bases on feature i's knot row (Cox-de Boor).
 //
-// One contraction over K = I * (1 + C') (C' = C rounded up to 8, 16 or 32) on the fp16
-// MFMA v_mfma_f32_16x16x32_f16 with a three-term split for fp32-level accuracy: every
-// operand v is carried as hi = fp16(v) and lo = fp16(v - hi), and each product as
-// hi*hi + hi*lo + lo*hi (the dropped lo*lo term is ~2^-22 relative), accumulated in fp32.
+// One contraction over K = I * (1 + C') (C' = C rounded up to 8 or 16) on the fp16 MFMA
+// v_mfma_f32_16x16x32_f16 with a three-term split for fp32-level accuracy: every operand v
+// is carried as hi = fp16(v) and lo = fp16(v - hi), and each product as hi*hi + lo*hi +
+// hi*lo (the dropped lo*lo term is ~2^-22 relative), accumulated in fp32.
 //
 // K order: features in groups of 32; each group is one "silu" chunk (32 features, k =
 // feature) followed by C' "spline" chunks; spline chunk t holds the C' bases of the 32/C'
@@ -15,16 +15,17 @@
 // of batch row l % 16, so over one group a lane needs x at one contiguous run of C'
 // features, and in a spline chunk it owns one (row, feature) and 8 of its bases: it finds
 // x's knot interval, evaluates the four bases nonzero there from per-interval cubic
-// coefficients and shifts them into its 8 slots, straight in registers — the expanded
-// activations never touch LDS or HBM.
+// coefficients and shifts them into its 8 slots.
 //
-// Per call, kan_prepare and kan_pack (a) write the weights ([Wb | Ws*sc], the A operand)
-// in that K order as fp16 hi/lo with a per-output-column power-of-two scale (so neither
-// half under- or overflows) and (b) tabulate each feature's knot row and per-interval
-// basis cubics.
-// The GEMM streams the weights through an LDS ring with direct-to-LDS loads, copies each
-// feature group's table into LDS, and undoes the column scale in the epilogue.
+// Per call: kan_prepare finds each output column's power-of-two scale (so neither fp16
+// half under- or overflows); kan_pack writes the weights ([Wb | Ws*sc], the A operand) in
+// that K order as scaled fp16 hi/lo, [chunk][column][32] so each chunk's tile is contiguous,
+// and tabulates every feature's knot row and per-interval basis cubics; kan_fused is the
+// warp-specialized GEMM (producer waves copy weight tiles and expand activations into LDS,
+// consumer waves run the MFMAs) and undoes the column scale in its epilogue.
 #pragma once
+
+#include <utility>
 
 #include "common.hpp"
 
@@ -33,22 +34,39 @@ namespace kan {
 
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;     // 4 waves, one per SIMD
-constexpr int kWaves = kThreads / 64;
-constexpr int BM = 128;           // batch rows per workgroup: 32 per wave = 2 row blocks
-constexpr int BN = 256;           // output columns per workgroup: 16 column blocks
-constexpr int kNJ = BN / 16;
 constexpr int kGroup = 32;        // features per group
 constexpr int kChunk = 32;        // k per MFMA chunk
 constexpr int kMaxKnots = 16;     // fast path: grid_size + 2*order + 1 <= 16
 constexpr int kOrder = 3;         // the fast path's spline order
-constexpr int kTileBytes = BN * kChunk * 2;          // one half (hi or lo) of a chunk tile: 16 KiB
-constexpr int kStageBytes = 2 * kTileBytes;          // hi + lo: 32 KiB
-constexpr int kGroupsPerWave = BN / 16 / kWaves;     // 16-row tile groups each wave copies
 constexpr int kRawBufferFlags = 0x00020000;
 constexpr unsigned kOutOfRange = 0x80000000u;
+
+// kan_fused tiling: a 128 x 256 output tile per workgroup of 8 waves.  Waves 0-3 are
+// consumers: wave w owns all 128 batch rows (8 row blocks of 16) x output columns
+// 64w .. 64w+63 (4 column blocks), 128 fp32 accumulators, and only reads LDS and issues
+// MFMAs.  Waves 4-7 are producers: producer p copies a quarter of each weight tile into
+// LDS and expands the activations of batch rows 32p .. 32p+31 (2 row blocks).  One
+// producer and one consumer share each SIMD.
+constexpr int kThreads = 512;
+constexpr int kConsumerWaves = 4;
+constexpr int BM = 128;
+constexpr int BN = 256;
+constexpr int kRB = BM / 16;                        // row blocks per tile (consumer)
+constexpr int kCB = BN / 16 / kConsumerWaves;       // column blocks per consumer wave
+constexpr int kWHalfBytes = BN * kChunk * 2;        // hi or lo weights of one chunk: 16 KiB
+constexpr int kWStageBytes = 2 * kWHalfBytes;       // one chunk's weight tile: 32 KiB
+constexpr int kWStages = 3;                         // weight ring: copies run two chunks ahead
+constexpr int kActBytes = kRB * 2 * 64 * 16;        // hi + lo activation fragments: 16 KiB
+constexpr int kActStages = 2;
+constexpr int kActAt = kWStages * kWStageBytes;
+constexpr int kTblAt = kActAt + kActStages * kActBytes;
+constexpr int kTblBytes = 32 * 1024;                // one group's table (L <= 16)
+constexpr int kLdsBytes = kTblAt + kTblBytes;       // 160 KiB
+static_assert(kLdsBytes <= 160 * 1024, "fits one CU's LDS");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, size_t bytes) {
   const int n = bytes > 0x7fffffffu ? 0x7fffffff : (int)bytes;
@@ -69,8 +87,6 @@ inline int padded_bases(int C) { return C <= 8 ? 8 : (C <= 16 ? 16 : (C <= 32 ? 
 // contributes nothing.  Layout: [group][tbl_group_bytes], feature fl of a group at
 // fl * 64 * L bytes, so one group is one contiguous copy.
 // ---------------------------------------------------------------------------------------
-constexpr int kTblBytes = 32 * 1024;  // LDS table buffer: 32 features * 64 * L bytes, L <= 16
-
 __host__ __device__ inline int tbl_group_bytes(int L) { return 4096 * ((L + 1) / 2); }
 
 // Position of basis r's 16-byte coefficient chunk within interval j's 64 bytes: XOR-ed
@@ -138,7 +154,7 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 // [2^14, 2^15), so neither fp16 half under- or overflows.
 // ---------------------------------------------------------------------------------------
 // kan_prepare: workgroup o reduces column o (contiguous rows of wb, sc and ws) to
-// colscale[o].  Workgroup 0 also zeroes kan_gemm's split-K arrival counters (their place in
+// colscale[o].  Workgroup 0 also zeroes kan_fused's split-K arrival counters (their place in
 // the workspace moves with the shape, so every call starts them from zero).
 __global__ __launch_bounds__(256) void kan_prepare(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
@@ -279,28 +295,6 @@ __global__ __launch_bounds__(256) void kan_pack(
 }
 
 // ---------------------------------------------------------------------------------------
-// GEMM with the fused activation expansion.
-//
-// 128x256 output tile per workgroup of 4 waves (one per SIMD); wave w owns batch rows
-// 32w..32w+31 (2 row blocks) x all 256 columns (16 column blocks, 128 fp32 accumulators in
-// AGPRs).  Weights stream through a 4-stage LDS ring of 32 KiB chunks (32 k x 256 columns,
-// hi then lo) filled by direct-to-LDS copies three chunks ahead; the group's table
-// (knots + cubics, <= 32 KiB) has one LDS buffer, copied at the previous group's last
-// chunk — when that group's last spline chunk has been expanded — before that chunk's
-// weight copy, so the group's first chunk waits for it.  x values are prefetched into
-// registers one group ahead.
-//
-// The activations of chunk q+1 are built during chunk q's MFMAs.  A wave issues its MFMAs
-// in order and cannot pass an outstanding wait, so each chunk runs in four quarters of 24
-// MFMAs (4 column blocks, weight fragments read a quarter ahead): the next chunk's knot
-// rows are read before Q1, whose MFMAs cover that latency; the interval lookup is
-// interleaved with Q2's MFMAs and issues the coefficient reads, which the rest of Q2
-// covers; the cubic evaluation, split and slot routing of row block 0 are interleaved
-// with Q3's MFMAs and those of row block 1 with Q4's.  The loop body is
-// one whole feature group unrolled (every chunk kind and wait count is a constant) and
-// weight and table copies past the end zero-fill through the buffer descriptors, so no
-// branch surrounds the MFMAs (which would make the compiler copy the accumulators).
-// ---------------------------------------------------------------------------------------
 // Weight tiles: 64-byte rows (32 fp16 of k); chunk c of row r sits at chunk c ^ ((r >> 1)
 // & 3), which spreads the 16 rows x 4 chunks of one fragment read over all banks
 // (measured on MI355X: 141 B/clk/CU against 127 unswizzled or with (r >> 2) & 3).
@@ -311,25 +305,6 @@ __device__ __forceinline__ int swizzle64(int row, int chunk) {
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-}
-
-// Copy part `part` (0 .. kGroupsPerWave-1) of this wave's share of chunk q's hi and lo
-// tiles (rows n0..n0+BN-1 of [q][Opad][32]) into an LDS stage: one 16-row group of each
-// half.  A direct-to-LDS instruction writes 64 consecutive 16-byte slots (16 rows of 64
-// bytes); lane i fetches the chunk the swizzle places in slot i.
-__device__ __forceinline__ void dma_chunk_part(__amdgpu_buffer_rsrc_t rhi, __amdgpu_buffer_rsrc_t rlo,
-                                               uint8_t* stage, int q, int Opad, int n0, int wave,
-                                               int lane, int part) {
-  const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
-  static_assert(kGroupsPerWave * kWaves * 16 == BN, "tile rows split evenly over waves");
-  const int group = wave * kGroupsPerWave + part;
-  const int row = group * 16 + r16;
-  const unsigned off = (unsigned)(((size_t)q * Opad + n0 + row) * 64 + 16 * logical);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      rhi, (__attribute__((address_space(3))) void*)(stage + group * 1024), 16, off, 0, 0, 0);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      rlo, (__attribute__((address_space(3))) void*)(stage + kTileBytes + group * 1024), 16, off,
-      0, 0, 0);
 }
 
 template <int n>
@@ -347,8 +322,6 @@ __device__ __forceinline__ float silu(float x) {
 // one fp32 value: otherwise the compiler may fuse the producer's last multiply with the
 // rounding of hi (one rounding of the exact product) while lo is still taken from the
 // fp32-rounded v, and hi + lo then misses v by an fp16 ulp in rare cases.
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ void split8(const float* v, f16x8& hi, f16x8& lo) {
 #pragma unroll
   for (int s = 0; s < 8; s += 2) {
@@ -439,8 +412,12 @@ __device__ __forceinline__ void tab_finish(float x, const TabFetch& t, int b0, f
   asm volatile("" : "+v"(N[0]), "+v"(N[1]), "+v"(N[2]), "+v"(N[3]));
   const f16x2 h01 = __builtin_convertvector(f32x2{N[0], N[1]}, f16x2);
   const f16x2 h23 = __builtin_convertvector(f32x2{N[2], N[3]}, f16x2);
-  const f16x2 l01 = __builtin_convertvector(f32x2{N[0] - (float)h01.x, N[1] - (float)h01.y}, f16x2);
-  const f16x2 l23 = __builtin_convertvector(f32x2{N[2] - (float)h23.x, N[3] - (float)h23.y}, f16x2);
+  // lo = fp16(N - hi), the difference exact in fp32: one v_fma_mix per value.
+  f16x2 l01, l23;
+  l01.x = (_Float16)__builtin_fmaf((float)h01.x, -1.0f, N[0]);
+  l01.y = (_Float16)__builtin_fmaf((float)h01.y, -1.0f, N[1]);
+  l23.x = (_Float16)__builtin_fmaf((float)h23.x, -1.0f, N[2]);
+  l23.y = (_Float16)__builtin_fmaf((float)h23.y, -1.0f, N[3]);
   const unsigned H0 = __builtin_bit_cast(unsigned, h01), H1 = __builtin_bit_cast(unsigned, h23);
   const unsigned L0 = __builtin_bit_cast(unsigned, l01), L1 = __builtin_bit_cast(unsigned, l23);
   unsigned m0, m1, m2, m3;  // slot masks: slots 2d, 2d+1 take fp16 halves of dword d % 2
@@ -474,330 +451,457 @@ __device__ __forceinline__ void tab_finish(float x, const TabFetch& t, int b0, f
 // b % nsplit, feature groups [split*gper, split*gper + gper), of tile b / nsplit.  It
 // writes its fp32 partial tile to `partial` and arrives on the tile's counter; the last
 // of the tile's nsplit arrivals sums the partials in split order (so the result does not
-// depend on which arrives last) and writes the output.
-template <int kCp, bool kVec, bool kUniform>
-__device__ __forceinline__ void kan_gemm_body(
-    uint8_t* smem, const float* __restrict__ x, const float* __restrict__ tables, int B, int I, int O,
-    int L, int ngroups, int Opad, const _Float16* __restrict__ bhi, const _Float16* __restrict__ blo,
-    const float* __restrict__ colscale, float* __restrict__ out, int nsplit, int gper,
-    float* __restrict__ partial, unsigned* __restrict__ counters) {
-  constexpr int kStages = 4;
-  constexpr int kQ = 1 + kCp;                        // chunks per feature group
-  constexpr int kPerStep = 2 * kGroupsPerWave;        // weight copy instructions per wave per chunk
-  constexpr int kX = kCp;                             // x values per lane and row block per group
-  uint8_t* tbl = smem + kStages * kStageBytes;
-  const int tm = (B + BM - 1) / BM, tn = Opad / BN;
-  const int split = blockIdx.x % nsplit, tile = blockIdx.x / nsplit;
-  const int g0 = split * gper, g1 = min(ngroups, g0 + gper);
-  int mt, nt;
-  tile_of(tile, tm, tn, mt, nt);
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  const int nq = ngroups * kQ;
-  const size_t tile_bytes = (size_t)nq * Opad * kChunk * 2;
-  const __amdgpu_buffer_rsrc_t rhi = make_rsrc(bhi, tile_bytes);
-  const __amdgpu_buffer_rsrc_t rlo = make_rsrc(blo, tile_bytes);
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, (size_t)B * I * 4);
-  const int tgb = tbl_group_bytes(L), tper = tgb / 4096;  // 1 KiB table copies per wave per group
-  const __amdgpu_buffer_rsrc_t rt = make_rsrc(tables, (size_t)ngroups * tgb);
-  const int fr = lane % 16, fg = lane / 16;
-  const int row0 = m0 + wave * 32;
 
-  f32x4 acc[2][kNJ];
+// ---------------------------------------------------------------------------------------
+// kan_fused: the warp-specialized GEMM.
+//
+// LDS (kLdsBytes):
+//   weight ring, 3 x 32 KiB: hi then lo, 256 rows (output columns of the tile) x 64 B
+//     (32 k) each, swizzle64
+//   activation fragments, 2 x 16 KiB: [row block 0..7][hi, lo][lane] x 16 B, exactly the B
+//     operand a consumer lane feeds its MFMA (one conflict-free 16-byte read)
+//   the basis table of the groups in use, 32 KiB
+//
+// Chunk c of the workgroup's range is computed by the consumers from weight stage c % 3 and
+// activation stage c % 2 while the producers write chunk c + 1's activations (evaluated in
+// registers) and copy chunk c + 2's weight tile (direct-to-LDS), so copies have two chunks
+// to land.  One workgroup barrier per chunk hands the stages over.  x is loaded one group
+// ahead.  Spline chunk t of a group reads the table entries of its own features only (the
+// features xb + t of the lanes), so once a chunk has been prepared its features' entries
+// are refilled with the next group's, a step later.
+// ---------------------------------------------------------------------------------------
+// Chunk c's weight tile (rows n0 .. n0 + 255 of [q][Opad][32], hi and lo) into weight stage
+// c % 3: one of the four copying waves (part) copies the 16-row groups 4 part .. 4 part + 3
+// of each half.  A direct-to-LDS instruction writes 64 consecutive 16-byte slots (16 rows of
+// 64 bytes); lane i fetches the chunk the swizzle places in slot i.  kPieces splits the 8
+// copy instructions so a caller can interleave them with other work.
+constexpr int kWeightCopies = 2 * (BN / 16) / 4;  // 1 KiB copies per copying wave per chunk
+template <int kPiece, int kPieces>
+__device__ __forceinline__ void copy_weight_tile(uint8_t* smem, __amdgpu_buffer_rsrc_t rhi, __amdgpu_buffer_rsrc_t rlo,
+                                                 int q, int c, int Opad, int n0, int part, int lane) {
+  uint8_t* st = smem + (c % kWStages) * kWStageBytes;
+  const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
+  constexpr int kPer = kWeightCopies / 2 / kPieces;
 #pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int j = 0; j < kNJ; ++j) acc[rb][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = kPiece * kPer; i < (kPiece + 1) * kPer; ++i) {
+    const int group = part * (kWeightCopies / 2) + i;
+    const unsigned off = (unsigned)(((size_t)q * Opad + n0 + group * 16 + r16) * 64 + 16 * logical);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rhi, (__attribute__((address_space(3))) void*)(st + group * 1024), 16, off, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        rlo, (__attribute__((address_space(3))) void*)(st + kWHalfBytes + group * 1024), 16, off, 0, 0, 0);
+  }
+}
 
-  // This lane's features within a group are xb .. xb + kX - 1 (slot t = feature xb + t):
-  // spline chunk t expands feature xb + t, and the silu chunk's features 8*fg .. +7 are
-  // slots 8*fg - xb .. +7.
-  const int xb = ((8 * fg) / kCp) * kCp;
-  float xcur[2][kX], xnext[2][kX];
-  auto prefetch = [&](int g) {  // past I or B: reads as 0 (against zero weights)
+template <int kCp, bool kVec>
+struct Producer {
+  static constexpr int kQ = 1 + kCp;
+  static constexpr int kX = kCp;                                    // x values per row block per group
+  static constexpr int kCopies = kWeightCopies;
+  static constexpr int kTableCopies = kTblBytes / 1024 / 4;         // 1 KiB table copies per producer wave
+  static constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;       // x load instructions per group
+  static_assert(2 * kCopies + kTableCopies + kXLoads + 1 <= 63, "vmcnt holds at most 63");
+
+  uint8_t* smem;
+  __amdgpu_buffer_rsrc_t rhi, rlo, rx, rt;
+
+  __device__ __forceinline__ void copy_weights(int c) const {
+    copy_weight_tile<0, 1>(smem, rhi, rlo, (g0 + c / kQ) * kQ + c % kQ, c, Opad, n0, pw, lane);
+  }
+
+  // Piece kPiece of 4 of chunk c's weight copies (none past the last chunk).
+  template <int kPiece>
+  __device__ __forceinline__ void copy_weights_piece(int c) const {
+    if (c < nchunks) copy_weight_tile<kPiece, 4>(smem, rhi, rlo, (g0 + c / kQ) * kQ + c % kQ, c, Opad, n0, pw, lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  int I, L, B, Opad, n0;
+  int g0, nlg, nchunks;
+  int lane, fr, fg, pw, xb;
+  int row[2];      // this lane's batch rows (global) for its two row blocks
+  bool uniform;    // every knot row is uniform: direct interval lookup
+  int tgb;
+
+  // Group lg's whole table into the table buffer: producer wave pw copies 1 KiB blocks
+  // kTableCopies * pw .. +kTableCopies - 1; blocks past the group's table zero-fill.
+  __device__ __forceinline__ void copy_table(int lg) const {
+    uint8_t* dst = smem + kTblAt;
+    const int g = g0 + lg;
+#pragma unroll
+    for (int i = 0; i < kTableCopies; ++i) {
+      const int blk = pw * kTableCopies + i;
+      const unsigned off = blk * 1024 < tgb ? (unsigned)((size_t)g * tgb + blk * 1024 + lane * 16) : kOutOfRange;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rt, (__attribute__((address_space(3))) void*)(dst + blk * 1024), 16, off, 0, 0, 0);
+    }
+  }
+
+  // The entries of spline chunk t's features (t + kCp * m, m < 32 / kCp) of group lg into
+  // the table buffer: producer wave pw < 32 / kCp copies feature t + kCp * pw, whose 64 L
+  // bytes are 4 L lanes of one direct-to-LDS instruction.
+  __device__ __forceinline__ void copy_table_slice(int lg, int t) const {
+    if (lane < 4 * L) {
+      const int fl = t + kCp * pw;
+      const unsigned off = (unsigned)((size_t)(g0 + lg) * tgb + fl * 64 * L + lane * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rt, (__attribute__((address_space(3))) void*)(smem + kTblAt + fl * 64 * L), 16, off, 0, 0, 0);
+    }
+  }
+
+  // x at this lane's features xb .. xb + kX - 1 of group lg (past I or B: 0).
+  __device__ __forceinline__ void load_x(int lg, float (&xs)[2][kX]) const {
+    const int g = g0 + lg;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int row = row0 + rb * 16 + fr;
       if constexpr (kVec) {  // I % 4 == 0: a 4-feature run is wholly inside or past I
 #pragma unroll
         for (int v = 0; v < kX / 4; ++v) {
           const int f = g * kGroup + xb + 4 * v;
-          const unsigned off = (row < B && f < I) ? (unsigned)((row * I + f) * 4) : kOutOfRange;
+          const unsigned off = (row[rb] < B && f < I) ? (unsigned)(((size_t)row[rb] * I + f) * 4) : kOutOfRange;
           const f32x4 val = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
 #pragma unroll
-          for (int e = 0; e < 4; ++e) xnext[rb][4 * v + e] = val[e];
+          for (int e = 0; e < 4; ++e) xs[rb][4 * v + e] = val[e];
         }
       } else {
 #pragma unroll
         for (int t = 0; t < kX; ++t) {
           const int f = g * kGroup + xb + t;
-          const unsigned off = (row < B && f < I) ? (unsigned)((row * I + f) * 4) : kOutOfRange;
-          xnext[rb][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
+          const unsigned off = (row[rb] < B && f < I) ? (unsigned)(((size_t)row[rb] * I + f) * 4) : kOutOfRange;
+          xs[rb][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
         }
       }
     }
-  };
-  auto dma_part = [&](int q, int part) {
-    dma_chunk_part(rhi, rlo, smem + (q % kStages) * kStageBytes, q, Opad, n0, wave, lane, part);
-  };
-  auto dma = [&](int q) {
-#pragma unroll
-    for (int i = 0; i < kGroupsPerWave; ++i) dma_part(q, i);
-  };
-  auto dma_table = [&](int g) {
-    for (int i = 0; i < tper; ++i) {
-      const int blk = wave * tper + i;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rt, (__attribute__((address_space(3))) void*)(tbl + blk * 1024), 16,
-          (unsigned)(g * tgb + blk * 1024 + lane * 16), 0, 0, 0);
-    }
-  };
-  auto silu_rb = [&](const float (&xs)[2][kX], int rb, f16x8& hi, f16x8& lo) {
-    float v[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      float xv = xs[rb][t];
-      if constexpr (kX > 8) xv = (fg & 1) ? xs[rb][8 + t] : xv;  // slot 8*fg - xb + t
-      v[t] = silu(xv);
-    }
-    split8(v, hi, lo);
-  };
-  auto silu_chunk = [&](const float (&xs)[2][kX], f16x8 (&hi)[2], f16x8 (&lo)[2]) {
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) silu_rb(xs, rb, hi[rb], lo[rb]);
-  };
-  // Row block rb's activations for the next chunk (a spline chunk from this group's table,
-  // or the next group's silu chunk).
-  auto expand_rb = [&](bool spline_next, int xs, const TabFetch& tf, int rb, f16x8& hi, f16x8& lo) {
-    if (spline_next)
-      tab_finish<kCp>(xcur[rb][xs], tf, (8 * fg) % kCp, hi, lo);
-    else
-      silu_rb(xnext, rb, hi, lo);
-  };
-
-  // Prologue: group g0's table, its first 3 weight chunks, its x, its silu activations.
-  dma_table(g0);
-#pragma unroll
-  for (int s = 0; s < kStages - 1; ++s) dma(g0 * kQ + s);
-  prefetch(g0);
-  f16x8 ahi[2], alo[2];
-  {
-    float x0[2][kX];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int t = 0; t < kX; ++t) x0[rb][t] = xnext[rb][t];
-    silu_chunk(x0, ahi, alo);
   }
 
-  constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;  // x load instructions per group
-  // vmcnt counts to 63; a smaller allowance only waits for more of the later loads.
-  constexpr int kW0 = kPerStep + kXLoads > 63 ? 63 : kPerStep + kXLoads;
-  constexpr int kW12 = 2 * kPerStep + kXLoads > 63 ? 63 : 2 * kPerStep + kXLoads;
-  for (int g = g0; g < g1; ++g) {
-    barrier_no_vm_drain();
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
-    prefetch(g + 1);
-#pragma unroll
-    for (int k = 0; k < kQ; ++k) {
-      const int q = g * kQ + k;
-      // Issue order: the table of group g and chunk q0+2 at the previous group's last
-      // chunk, the x prefetch at group start, chunk q+3 at chunk q.  Chunk q (and at k == 0
-      // the table) has landed once at most these later ones are outstanding.
-      if (k == 0) wait_vmcnt<kW0>();
-      else if (k <= 2) wait_vmcnt<kW12>();
-      else wait_vmcnt<2 * kPerStep>();
-      barrier_no_vm_drain();
-      if (k == kQ - 1) dma_table(g + 1);
-      // Chunk q+3 goes to the stage chunk q-1 used, which every wave has finished reading
-      // (barrier above).  Its copies are issued a part per quarter: issued together, the
-      // workgroup's 32 copy instructions queue at the memory pipeline and hold up the
-      // waves' MFMAs behind them.
-      static_assert(kGroupsPerWave == 4, "one copy part per quarter");
-      dma_part(q + kStages - 1, 0);
-
-      const uint8_t* st = smem + (q % kStages) * kStageBytes;
-      f16x8 wa[4][2], wb[4][2];
-      auto load_w = [&](int j0, f16x8 (&w)[4][2]) {
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int r = (j0 + u) * 16 + fr;
-          w[u][0] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(st + swizzle64(r, fg)));
-          w[u][1] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(st + kTileBytes + swizzle64(r, fg)));
-        }
-      };
-      // 4 column blocks x 2 row blocks x 3 split terms; weights are the A operand, so a
-      // block is [o][b] (lane: batch row fr, registers: 4 consecutive columns).  Issued
-      // term by term over the 8 blocks, so an accumulator's next MFMA is 8 MFMAs behind
-      // its previous one (each accumulator still sums hi*hi, lo*hi, hi*lo in that order).
-      auto mfma_w = [&](int j0, const f16x8 (&w)[4][2]) {
-#pragma unroll
-        for (int term = 0; term < 3; ++term)
-#pragma unroll
-          for (int u = 0; u < 4; ++u)
-#pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-              acc[rb][j0 + u] = mfma16(term == 1 ? w[u][1] : w[u][0], term == 2 ? alo[rb] : ahi[rb], acc[rb][j0 + u]);
-      };
-      // The next chunk: this group's spline chunk k+1, or the next group's silu chunk.
-      const bool spline_next = k + 1 < kQ;
-      const int fl = spline_next ? xb + k : 0;  // feature in group
-      const float* fe = reinterpret_cast<const float*>(tbl + fl * 64 * L);
-      const int xs = spline_next ? k : 0;
-      f16x8 nhi[2], nlo[2];
-      f32x4 kn[4];
-      f32x2 k01;
-      TabFetch tf[2];
-      load_w(0, wa);
-      if (spline_next) {
-        if constexpr (kUniform) k01 = *reinterpret_cast<const f32x2*>(fe);
-        else tab_knots(fe, kn);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      mfma_w(0, wa);  // Q1
-      load_w(4, wb);
-      __builtin_amdgcn_sched_barrier(0);
-      dma_part(q + kStages - 1, 1);
-      if (spline_next) {
-        if constexpr (kUniform) {
-          const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_uniform(xcur[rb][xs], k01.x, inv_h, fe, L);
-        } else {
-#pragma unroll
-          for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_count(xcur[rb][xs], kn, fe, L);
-        }
-      }
-      mfma_w(4, wb);  // Q2, interleaved with the interval lookup, which issues the coefficient reads
-      load_w(8, wa);
-#pragma unroll
-      for (int u = 0; u < 24; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // 2 VALU
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      dma_part(q + kStages - 1, 2);
-      expand_rb(spline_next, xs, tf[0], 0, nhi[0], nlo[0]);
-      mfma_w(8, wa);  // Q3, interleaved with row block 0's evaluation
-      load_w(12, wb);
-#pragma unroll
-      for (int u = 0; u < 24; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      dma_part(q + kStages - 1, 3);
-      expand_rb(spline_next, xs, tf[1], 1, nhi[1], nlo[1]);
-      mfma_w(12, wb);  // Q4, interleaved with row block 1's
-#pragma unroll
-      for (int u = 0; u < 24; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // 3 VALU
-      }
-      __builtin_amdgcn_sched_barrier(0);
+  // Chunk c's activations into stage c % 2: the lane's two row blocks evaluated, split and
+  // stored as their MFMA fragments.  A silu chunk (kT < 0) takes slots 8 fg .. 8 fg + 7 from
+  // the lane's x values 8 fg - xb ..; spline chunk kT expands feature xb + kT.
+  // The weight copies of chunk cw are issued in four pieces between the parts of the
+  // evaluation: a copy instruction holds the wave until the CU's memory pipeline takes it,
+  // so spreading them lets the evaluation's VALU work fill that time.
+  template <int kT>
+  __device__ __forceinline__ void prepare_act(int c, const float (&xs)[2][kX], int cw, f32x2& k01next) const {
+    uint8_t* act = smem + kActAt + (c & 1) * kActBytes;
+    copy_weights_piece<0>(cw);
+    // Both row blocks are evaluated before either is stored: a store to LDS orders every
+    // later LDS read after it, so interleaving would serialise the two lookups.
+    f16x8 hi[2], lo[2];
+    if constexpr (kT < 0) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
-        ahi[rb] = nhi[rb];
-        alo[rb] = nlo[rb];
+        float a[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          float xv = xs[rb][t];
+          if constexpr (kX > 8) {
+            // Both candidates as register values first: a select between two elements would
+            // otherwise become a runtime index, which keeps the array in scratch memory.
+            float xh = xs[rb][8 + t];
+            asm volatile("" : "+v"(xv), "+v"(xh));
+            xv = (fg & 1) ? xh : xv;
+          }
+          a[t] = silu(xv);
+        }
+        split8(a, hi[rb], lo[rb]);
+        if (rb == 0) copy_weights_piece<1>(cw);
       }
+      copy_weights_piece<2>(cw);
+    } else {
+      const float* fe = reinterpret_cast<const float*>(smem + kTblAt + (xb + kT) * 64 * L);
+      TabFetch tf[2];
+      if (uniform) {
+        // The first two knots were read a step ago (k01); read the next spline chunk's now.
+        const f32x2 k01 = k01next;
+        k01next = *reinterpret_cast<const f32x2*>(smem + kTblAt + (xb + (kT + 1) % kX) * 64 * L);
+        const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_uniform(xs[rb][kT], k01.x, inv_h, fe, L);
+      } else {
+        f32x4 kn[4];
+        tab_knots(fe, kn);
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_count(xs[rb][kT], kn, fe, L);
+      }
+      copy_weights_piece<1>(cw);
+      tab_finish<kCp>(xs[0][kT], tf[0], (8 * fg) % kCp, hi[0], lo[0]);
+      copy_weights_piece<2>(cw);
+      tab_finish<kCp>(xs[1][kT], tf[1], (8 * fg) % kCp, hi[1], lo[1]);
     }
-  }
-  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
-
-  if (nsplit > 1) {
-    // This thread's 16-byte slots of the tile: (wave, rb, j, lane), so every store and
-    // load instruction of a wave covers 1 KiB of contiguous memory.
-    constexpr int kTileFloats = BM * BN;
-    auto slot = [&](int rb, int j) { return (((wave * 2 + rb) * kNJ + j) * kWave + lane) * 4; };
-    const int tiles = gridDim.x / nsplit;
-    float* mine = partial + ((size_t)split * tiles + tile) * kTileFloats;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int j = 0; j < kNJ; ++j) *reinterpret_cast<f32x4*>(mine + slot(rb, j)) = acc[rb][j];
-    __syncthreads();  // every wave's stores have completed to L2; the LDS ring is idle
-    unsigned* flag = reinterpret_cast<unsigned*>(smem);
-    if (tid == 0) {
-      // Release at agent scope (writes the partial back past this XCD's L2), then arrive.
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      const unsigned prev = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *flag = prev == (unsigned)nsplit - 1;
-    }
-    __syncthreads();
-    if (!*flag) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const size_t split_stride = (size_t)tiles * kTileFloats;
-    const float* first = partial + (size_t)tile * kTileFloats;
-    // Split by split, all 32 of the thread's slots at once, so the loads of a split are in
-    // flight together; each slot sums splits 0, 1, ... in order, this workgroup's own split
-    // from its registers.
-    f32x4 own[2][kNJ];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int j = 0; j < kNJ; ++j) own[rb][j] = acc[rb][j];
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const float* src = first + sp * split_stride;
-      f32x4 part[2][kNJ];
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int j = 0; j < kNJ; ++j)
-          part[rb][j] = sp == split ? own[rb][j] : *reinterpret_cast<const f32x4*>(src + slot(rb, j));
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-        for (int j = 0; j < kNJ; ++j) acc[rb][j] = sp == 0 ? part[rb][j] : acc[rb][j] + part[rb][j];
-    }
-  }
-
-  // Epilogue: lane holds columns n0 + 16j + 4*fg + 0..3 of batch row row0 + 16rb + fr.
-  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, (size_t)B * O * 4);
-#pragma unroll
-  for (int j = 0; j < kNJ; ++j) {
-    const int o = n0 + j * 16 + 4 * fg;
-    const f32x4 cs = *reinterpret_cast<const f32x4*>(colscale + o);
+    copy_weights_piece<3>(cw);
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int row = row0 + rb * 16 + fr;
-      const f32x4 val = acc[rb][j] * cs;
-      if constexpr (kVec) {
-        const unsigned off = (row < B && o < O) ? (unsigned)((row * O + o) * 4) : kOutOfRange;
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val), ro, off, 0, 0);
-      } else {
+      const int frag = 2 * pw + rb;
+      *reinterpret_cast<f16x8*>(act + ((frag * 2 + 0) * 64 + lane) * 16) = hi[rb];
+      *reinterpret_cast<f16x8*>(act + ((frag * 2 + 1) * 64 + lane) * 16) = lo[rb];
+    }
+  }
+
+  // Step lg * kQ + kK runs while the consumers compute that chunk: it refills the entries
+  // of the spline chunk prepared in the previous step with the next group's, loads the next
+  // group's x at a group's first step, and writes the activations of chunk c = lg * kQ +
+  // kK + 1 (spline chunk kK of group lg, or for kK = kQ - 1 the next group's silu chunk).
+  // kLast: lg is the workgroup's last group.  Every condition is a constant, so
+  // the compiler's own waits for x stay exact (a merge of paths would make it wait for
+  // every load, the weight copies of the step included).
+  template <bool kLast, int kK>
+  __device__ __forceinline__ void step(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX], f32x2& k01) const {
+    const int c = lg * kQ + kK + 1;
+    constexpr bool kCopyNext = !kLast || kK + 2 < kQ;   // chunk c + 1 exists
+    constexpr bool kSlice = !kLast && kK >= 1;          // refill spline chunk kK - 1's entries
+    constexpr bool kXNext = !kLast && kK == 0;
+    // (only the waves with a feature of the slice issue its copy)
+    const bool slice = kSlice && pw < kGroup / kCp;
+    if (slice) copy_table_slice(lg + 1, kK - 1);
+    if constexpr (kXNext) load_x(lg + 1, xnext);
+    if constexpr (kK < kQ - 1) {
+      prepare_act<kK>(c, xcur, c + 1, k01);
+    } else if constexpr (!kLast) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const unsigned off = (row < B && o + e < O) ? (unsigned)((row * O + o + e) * 4) : kOutOfRange;
-          // Through a scalar: hipcc turned __builtin_bit_cast(unsigned, val[e]) into a store of
-          // element 0 for every e.
-          const float ve = val[e];
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ve), ro, off, 0, 0);
-        }
+      for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
+      prepare_act<-1>(c, xcur, c + 1, k01);
+    } else {
+      copy_weights_piece<0>(c + 1);  // past the last chunk: no copies
+    }
+    // Everything issued before this step (chunk c's weights among it) has landed.
+    constexpr int kIssued = (kCopyNext ? kCopies : 0) + (kXNext ? kXLoads : 0);
+    if (slice) wait_vmcnt<kIssued + 1>();
+    else wait_vmcnt<kIssued>();
+    barrier_no_vm_drain();
+  }
+
+  template <bool kLast, int... kKs>
+  __device__ __forceinline__ void group_steps(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX], f32x2& k01,
+                                              std::integer_sequence<int, kKs...>) const {
+    (step<kLast, kKs>(lg, xcur, xnext, k01), ...);
+  }
+
+  __device__ void run() const {
+    float xcur[2][kX], xnext[2][kX];
+    // Prologue: chunks 0 and 1's weights, the first group's table and x, chunk 0's
+    // activations; the barrier after it publishes them.
+    copy_weights(0);
+    if (nchunks > 1) copy_weights(1);
+    copy_table(0);
+    load_x(0, xcur);
+    wait_vmcnt<0>();
+    f32x2 k01;
+    prepare_act<-1>(0, xcur, nchunks, k01);  // (no copies: chunk 1's were issued above)
+    barrier_no_vm_drain();
+    // Spline chunk 0's first two knots: the whole table is visible after the barrier.
+    k01 = *reinterpret_cast<const f32x2*>(smem + kTblAt + xb * 64 * L);
+    // The steps of a group are unrolled, so every chunk kind is a constant.
+    for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, k01, std::make_integer_sequence<int, kQ>{});
+    group_steps<true>(nlg - 1, xcur, xnext, k01, std::make_integer_sequence<int, kQ>{});
+  }
+};
+
+// Consumer: chunk c's 96 MFMAs, two row blocks at a time and term-major, so an
+// accumulator's next MFMA is 8 MFMAs behind its previous one (each accumulator sums
+// hi*hi, lo*hi, hi*lo per chunk, in that order).  The next pair's activation fragments are
+// read during a pair's MFMAs (one read per six MFMAs), so LDS reads overlap the MFMAs.
+__device__ __forceinline__ void consume_chunk(const uint8_t* wst, const uint8_t* ast, int wave, int lane,
+                                              f32x4 (&acc)[kRB][kCB]) {
+  const int fr = lane % 16, fg = lane / 16;
+  f16x8 wh[kCB], wl[kCB];
+#pragma unroll
+  for (int cb = 0; cb < kCB; ++cb) {
+    const int r = wave * (kCB * 16) + cb * 16 + fr;
+    wh[cb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(wst + swizzle64(r, fg)));
+    wl[cb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(wst + kWHalfBytes + swizzle64(r, fg)));
+  }
+  const uint8_t* act = ast + lane * 16;
+  auto read_pair = [&](int rb, f16x8 (&ah)[2], f16x8 (&al)[2]) {
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      ah[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(act + ((rb + r) * 2 + 0) * 1024));
+      al[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(act + ((rb + r) * 2 + 1) * 1024));
+    }
+  };
+  f16x8 ah[2], al[2];
+  read_pair(0, ah, al);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int rb = 0; rb < kRB; rb += 2) {
+    f16x8 nh[2], nl[2];
+    if (rb + 2 < kRB) read_pair(rb + 2, nh, nl);
+#pragma unroll
+    for (int term = 0; term < 3; ++term)
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb)
+          acc[rb + r][cb] = mfma16(term == 1 ? wl[cb] : wh[cb], term == 2 ? al[r] : ah[r], acc[rb + r][cb]);
+    if (rb + 2 < kRB) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);  // 6 MFMAs
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (rb + 2 < kRB) {
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        ah[r] = nh[r];
+        al[r] = nl[r];
       }
     }
   }
 }
 
-// The uniform-grid flags (one per table workgroup of kan_prepare) are read once; the branch
-// selects one of two whole loop bodies, so no branch sits inside the MFMA loop.
+// Output slot of a consumer accumulator: consumer wave wq, row block rb, column block cb,
+// lane lq hold columns n0 + 64 wq + 16 cb + 4 (lq / 16) + 0..3 of batch row m0 + 16 rb +
+// lq % 16, scaled back by the columns' scales.
+__device__ __forceinline__ void store_slot(f32x4 val, int wq, int rb, int cb, int lq, int m0, int n0, int B, int O,
+                                           const float* __restrict__ colscale, __amdgpu_buffer_rsrc_t ro, bool vec) {
+  const int o = n0 + wq * (kCB * 16) + cb * 16 + 4 * (lq / 16);
+  const int row = m0 + rb * 16 + lq % 16;
+  val *= *reinterpret_cast<const f32x4*>(colscale + o);
+  if (vec) {
+    const unsigned off = (row < B && o < O) ? (unsigned)(((size_t)row * O + o) * 4) : kOutOfRange;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val), ro, off, 0, 0);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const unsigned off = (row < B && o + e < O) ? (unsigned)(((size_t)row * O + o + e) * 4) : kOutOfRange;
+      // Through a scalar: hipcc turned __builtin_bit_cast(unsigned, val[e]) into a store of
+      // element 0 for every e.
+      const float ve = val[e];
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ve), ro, off, 0, 0);
+    }
+  }
+}
+
+// Split-K handover, all 512 threads: after every consumer has written its partial, thread 0
+// releases them at agent scope and arrives on the tile's counter; the tile's last arrival
+// sums the nsplit partials of every slot in split order (so the result does not depend on
+// which split arrives last), 16 slots per thread with each split's loads in flight
+// together, resets the counter and writes the output.
+template <bool kVec>
+__device__ __forceinline__ void split_k_finish(uint8_t* smem, int tid, int split, int nsplit, int tile, int m0,
+                                               int n0, int B, int O, const float* __restrict__ colscale,
+                                               float* __restrict__ out, const float* __restrict__ partial,
+                                               unsigned* __restrict__ counters) {
+  __syncthreads();  // every consumer's partial stores have completed; the LDS stages are idle
+  unsigned* flag = reinterpret_cast<unsigned*>(smem);
+  if (tid == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned prev = __hip_atomic_fetch_add(counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == (unsigned)nsplit - 1;
+    if (last) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (!*flag) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  constexpr int kSlots = BM * BN / 4;           // 16-byte slots per tile
+  constexpr int kPer = kSlots / kThreads;       // per thread
+  const int tiles = gridDim.x / nsplit;
+  const size_t split_stride = (size_t)tiles * (BM * BN);
+  const float* first = partial + (size_t)tile * (BM * BN);
+  f32x4 sum[kPer];
+  for (int sp = 0; sp < nsplit; ++sp) {
+    f32x4 part[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u)
+      part[u] = *reinterpret_cast<const f32x4*>(first + sp * split_stride + (size_t)(tid + u * kThreads) * 4);
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) sum[u] = sp == 0 ? part[u] : sum[u] + part[u];
+  }
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, (size_t)B * O * 4);
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int sl = tid + u * kThreads;  // = ((wq * kRB + rb) * kCB + cb) * 64 + lq
+    const int lq = sl % kWave, cb = (sl / kWave) % kCB, rb = (sl / (kWave * kCB)) % kRB, wq = sl / (kWave * kCB * kRB);
+    store_slot(sum[u], wq, rb, cb, lq, m0, n0, B, O, colscale, ro, kVec);
+  }
+}
+
+// kVec: I and O multiples of 4, x and out 16-byte aligned (16-byte loads and stores);
+// otherwise 4-byte ones.
+//
+// Split-K (nsplit > 1, for grids of fewer tiles than CUs): workgroup b computes split
+// b % nsplit, feature groups [split*gper, split*gper + gper), of tile b / nsplit.  It
+// writes its fp32 partial tile to `partial` and arrives on the tile's counter; the last
+// of the tile's nsplit arrivals sums the partials in split order (so the result does not
+// depend on which arrives last) and writes the output.
 template <int kCp, bool kVec>
-__global__ __launch_bounds__(kThreads) void kan_gemm(
-    const float* __restrict__ x, const float* __restrict__ tables, const int* __restrict__ uflags,
-    int nflags, int B, int I, int O, int L, int ngroups, int Opad, const _Float16* __restrict__ bhi,
+__global__ __launch_bounds__(kThreads) void kan_fused(
+    const float* __restrict__ x, const float* __restrict__ tables, const int* __restrict__ uflags, int nflags,
+    int B, int I, int O, int L, int ngroups, int Opad, const _Float16* __restrict__ bhi,
     const _Float16* __restrict__ blo, const float* __restrict__ colscale, float* __restrict__ out, int nsplit,
     int gper, float* __restrict__ partial, unsigned* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  bool ok = true;
-  for (int i = (int)threadIdx.x % kWave; i < nflags; i += kWave) ok = ok && uflags[i] != 0;
-  if (__builtin_amdgcn_ballot_w64(!ok) == 0)
-    kan_gemm_body<kCp, kVec, true>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit,
-                                   gper, partial, counters);
-  else
-    kan_gemm_body<kCp, kVec, false>(smem, x, tables, B, I, O, L, ngroups, Opad, bhi, blo, colscale, out, nsplit,
-                                    gper, partial, counters);
+  constexpr int kQ = 1 + kCp;
+  const int tm = (B + BM - 1) / BM, tn = Opad / BN;
+  const int split = blockIdx.x % nsplit, tile = blockIdx.x / nsplit;
+  const int g0 = split * gper, g1 = min(ngroups, g0 + gper);
+  const int nchunks = (g1 - g0) * kQ;
+  int mt, nt;
+  tile_of(tile, tm, tn, mt, nt);
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+
+  if (wave >= kConsumerWaves) {
+    {
+      Producer<kCp, kVec> p;
+      p.smem = smem;
+      p.I = I; p.L = L; p.B = B; p.Opad = Opad; p.n0 = n0;
+      p.g0 = g0; p.nlg = g1 - g0; p.nchunks = nchunks;
+      p.lane = lane; p.fr = lane % 16; p.fg = lane / 16; p.pw = wave - kConsumerWaves;
+      p.xb = ((8 * p.fg) / kCp) * kCp;
+      p.row[0] = m0 + 32 * p.pw + p.fr;
+      p.row[1] = p.row[0] + 16;
+      p.tgb = tbl_group_bytes(L);
+      const size_t wbytes = (size_t)ngroups * kQ * Opad * kChunk * 2;
+      p.rhi = make_rsrc(bhi, wbytes);
+      p.rlo = make_rsrc(blo, wbytes);
+      p.rx = make_rsrc(x, (size_t)B * I * 4);
+      p.rt = make_rsrc(tables, (size_t)ngroups * p.tgb);
+      bool ok = true;
+      for (int i = lane; i < nflags; i += kWave) ok = ok && uflags[i] != 0;
+      p.uniform = __builtin_amdgcn_ballot_w64(!ok) == 0;
+      p.run();
+    }
+    wait_vmcnt<0>();  // no copy may still be writing LDS past this point
+    if (nsplit > 1) split_k_finish<kVec>(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
+    return;
+  }
+
+  f32x4 acc[kRB][kCB];
+#pragma unroll
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  barrier_no_vm_drain();  // stage 0 is ready
+  for (int c = 0; c < nchunks; ++c) {
+    consume_chunk(smem + (c % kWStages) * kWStageBytes, smem + kActAt + (c & 1) * kActBytes, wave, lane, acc);
+    barrier_no_vm_drain();
+  }
+
+  if (nsplit > 1) {
+    // This thread's 16-byte slots of the partial tile: (wave, rb, cb, lane), so every
+    // store instruction of a wave covers 1 KiB of contiguous memory.
+    const int tiles = gridDim.x / nsplit;
+    float* mine = partial + ((size_t)split * tiles + tile) * (BM * BN);
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb)
+        *reinterpret_cast<f32x4*>(mine + (((wave * kRB + rb) * kCB + cb) * kWave + lane) * 4) = acc[rb][cb];
+    split_k_finish<kVec>(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
+    return;
+  }
+
+  // Epilogue.
+  const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, (size_t)B * O * 4);
+#pragma unroll
+  for (int cb = 0; cb < kCB; ++cb)
+#pragma unroll
+    for (int rb = 0; rb < kRB; ++rb) store_slot(acc[rb][cb], wave, rb, cb, lane, m0, n0, B, O, colscale, ro, kVec);
 }
 
 }  // namespace kan

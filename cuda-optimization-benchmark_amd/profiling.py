@@ -41,7 +41,7 @@ DOMINANT = {
     # <threads, unroll, vector loads, entropy, nt>: the entropy and the drop-in variants
     "ppo_clip": "ppo_clip_kernel<512, 2, true, true,",
     "ppo_clip_dropin": "ppo_clip_kernel<512, 2, true, false,",
-    "efficient_kan": "kan_gemm",
+    "efficient_kan": "kan_fused",
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny",
     "quantize_e4m3": "qz_fused",
