@@ -20,10 +20,27 @@ extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const 
   const int vec = vec_width(x_fp8, w_fp8, K);
   if (M <= kSkinnyMaxM) {
     const dim3 grid((N + 15) / 16);
-    if (vec == 16)
-      hipLaunchKernelGGL(fp8_gemm_skinny<16>, grid, dim3(kSkinnyThreads), 0, stream, x_fp8, w_fp8,
-                         (int)M, (int)N, (int)K, inv, bias, output);
-    else if (vec == 8)
+    if (vec == 16) {
+      // Flat loads through LDS; M decides the row blocks (and so the K slice per pass).
+      switch ((M + 15) / 16) {
+        case 1:
+          hipLaunchKernelGGL(fp8_gemm_skinny_flat<1>, grid, dim3(kSkinnyThreads), skinny_lds_bytes(1), stream,
+                             x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+          break;
+        case 2:
+          hipLaunchKernelGGL(fp8_gemm_skinny_flat<2>, grid, dim3(kSkinnyThreads), skinny_lds_bytes(2), stream,
+                             x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+          break;
+        case 3:
+          hipLaunchKernelGGL(fp8_gemm_skinny_flat<3>, grid, dim3(kSkinnyThreads), skinny_lds_bytes(3), stream,
+                             x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+          break;
+        default:
+          hipLaunchKernelGGL(fp8_gemm_skinny_flat<4>, grid, dim3(kSkinnyThreads), skinny_lds_bytes(4), stream,
+                             x_fp8, w_fp8, (int)M, (int)N, (int)K, inv, bias, output);
+          break;
+      }
+    } else if (vec == 8)
       hipLaunchKernelGGL(fp8_gemm_skinny<8>, grid, dim3(kSkinnyThreads), 0, stream, x_fp8, w_fp8,
                          (int)M, (int)N, (int)K, inv, bias, output);
     else

@@ -43,7 +43,7 @@ DOMINANT = {
     "ppo_clip_dropin": "ppo_clip_kernel<512, 2, true, false,",
     "efficient_kan": "kan_fused",
     "fp8_linear": "fp8_gemm_wide",
-    "fp8_linear_m16": "fp8_gemm_skinny",
+    "fp8_linear_m16": "fp8_gemm_skinny_flat",
     "quantize_e4m3": "qz_fused",
 }
 COPY_PROBE_BYTES = 256 << 20

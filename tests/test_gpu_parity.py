@@ -145,7 +145,8 @@ def test_efficient_kan_shapes(lib, shape):
 # (M, K, N, output offset in bf16 elements).  K % 16 == 0 with 16-byte aligned operands
 # runs the wide kernel: its three epilogues (N % 8 == 0 and a 16-byte aligned output; N % 4
 # == 0 and 8-byte aligned; otherwise), M and N tile tails, K not a multiple of its 128-wide
-# step.  K % 16 != 0 runs the tiled kernel; M <= 64 the skinny.
+# step.  K % 16 != 0 runs the tiled kernel; M <= 64 the skinny (flat loads through LDS when
+# K % 16 == 0, loads in the MFMA layout otherwise).
 FP8_SHAPES = [
     (300, 192, 264, 0),
     (300, 192, 264, 4),
@@ -154,6 +155,16 @@ FP8_SHAPES = [
     (333, 1000, 300, 0),
     (65, 40, 33, 1),
     (64, 4096, 96, 0),
+    # skinny, flat 16-byte path: one to four row blocks (K slices of 512, 256, 256 and 128
+    # bytes), K past the last whole slice, N past the last 16-column block
+    (16, 4096, 272, 0),
+    (17, 528, 100, 0),
+    (40, 2064, 64, 2),
+    (33, 48, 20, 0),
+    (1, 16, 1, 0),
+    (49, 400, 130, 0),
+    # skinny with K % 16 != 0 (the register path)
+    (5, 40, 7, 0),
 ]
 
 
