@@ -46,7 +46,7 @@ MALL_BYTES = 256 << 20
 
 # op key -> (entry op, BASELINE key, bound, algorithmic work per call, dtype, description)
 WORKLOADS = {
-    "reward_to_go": ("reward_to_go", "reward_to_go", "hbm", 150_994_944, "f64",
+    "reward_to_go": ("reward_to_go", "reward_to_go", "hbm", 150_994_944, "f32 lane steps, f64 scans/carries",
                      "reward_to_go B=4096 T=4096 gamma=0.99 done_p=0.01 (BASELINE configs[1])"),
     "pow_abs_sqrt_mean": ("pow_abs_sqrt_mean", "pow_abs_sqrt_mean", "hbm", 536_870_916, "f32",
                           "pow_abs_sqrt_mean inp,target fp32 [16,4,1024,1024] N(0,1)"),
@@ -182,8 +182,10 @@ def time_cpu(op, inp, budget_s=10.0, max_reps=6):
 
 
 def _profile_json(name):
-    """A {bench op key: value} summary kept under profiles/ (traffic.json: HBM bytes per
-    launch; mfma.json: MFMA busy % of the dominant kernel), or {}."""
+    """A summary kept under profiles/ (traffic.json: HBM bytes per launch of each op's
+    dominant kernel and per call; mfma.json: MFMA busy % of the dominant kernel), written by
+    profiling.py from rocprofv3 counter runs, or {}.  These figures are not measured by
+    this run: each one bench reports carries a note naming the file and commit."""
     p = ROOT / "profiles" / name
     if p.exists():
         try:
@@ -191,6 +193,11 @@ def _profile_json(name):
         except json.JSONDecodeError:
             return {}
     return {}
+
+
+def _provenance(summary: dict, name: str) -> str:
+    return (f"from profiles/{name} ({summary.get('source') or 'rocprofv3 counters'}, "
+            f"commit {summary.get('commit') or 'unknown'}); not measured by this run")
 
 
 def main() -> int:
@@ -255,9 +262,14 @@ def main() -> int:
                     "frac": round(achieved / peak, 4)}
             if dtype in MFMA_PASSES:
                 roof["ceiling_frac"] = round(1.0 / MFMA_PASSES[dtype], 4)
-            if key in mfma_busy:
-                roof["mfma_busy_pct"] = mfma_busy[key]  # rocprofv3 counters, profiles/mfma_utilisation.md
-        roof["traffic"] = traffic.get(key)
+            if key in mfma_busy.get("values", {}):
+                roof["mfma_busy_pct"] = mfma_busy["values"][key]
+                roof["mfma_busy_pct_source"] = _provenance(mfma_busy, "mfma.json")
+        roof["traffic"] = traffic.get("values", {}).get(key)
+        if roof["traffic"] is not None:
+            roof["traffic_source"] = _provenance(traffic, "traffic.json")
+        if key in traffic.get("call_values", {}):
+            roof["call_traffic"] = traffic["call_values"][key]  # every kernel of one call
         r = {"workload": desc, "us_per_call": round(us, 3), "dtype": dtype,
              "algorithmic_" + ("bytes" if bound == "hbm" else "flop"): work,
              "timing": f"{'cold' if n > 1 else 'resident'}: {n} rotating input copies, {a.steps} calls",

@@ -2,9 +2,9 @@
 //
 // Drop-in signature tasks/efficient_kan/tests/task.json:3, replacing
 // reference/efficient_kan/solution.cu:177-288.  Fast path (efficient_kan.hpp): spline
-// order 3 with at most 16 knots per feature — kan_prepare (column scales), kan_pack (the
-// scaled fp16 hi/lo weights in the GEMM's K order, basis tables) and the warp-specialized
-// fp16x3 MFMA GEMM kan_fused.  Other shapes take the row-wise fp32 path below.
+// order 3 with at most 16 knots per feature — kan_pack (column scales, the scaled fp16
+// hi/lo weights in the GEMM's K order, basis tables) and the warp-specialized fp16x3 MFMA
+// GEMM kan_fused.  Other shapes take the row-wise fp32 path below.
 #include <algorithm>
 
 #include "efficient_kan.hpp"
@@ -81,7 +81,7 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const int nq = ngroups * (1 + kCp);
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
-  const int table_blocks = (ngroups * kGroup * L + 255) / 256;  // one thread per table entry
+  const int table_blocks = (ngroups * kGroup * L + kPackThreads - 1) / kPackThreads;  // a thread per entry
   // Split-K when the output tiles leave CUs idle (one workgroup fills a CU's LDS): up to
   // CUs / tiles splits of the feature groups, none empty.
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
@@ -105,14 +105,11 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   auto* uflags = reinterpret_cast<int*>(colscale + Opad);
   auto* counters = reinterpret_cast<unsigned*>(static_cast<char*>(wsp) + counters_at);
   auto* partial = reinterpret_cast<float*>(static_cast<char*>(wsp) + partial_at);
-  // One launch finds the column scales; the next packs the weights and builds the basis
-  // tables and their uniform-grid flags.
-  hipLaunchKernelGGL(kan_prepare, dim3(Opad), dim3(256), 0, stream, wb, ws, sc, I, O, C, colscale, counters,
+  // One launch finds the column scales, packs the weights and builds the basis tables and
+  // their uniform-grid flags.
+  hipLaunchKernelGGL(kan_pack<kCp>, dim3(table_blocks + Opad / kPackCols), dim3(kPackThreads), 0, stream, wb, ws,
+                     sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags, counters,
                      nsplit > 1 ? tiles : 0);
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(kan_pack<kCp>, dim3(table_blocks + (Opad / kPackCols) * ngroups), dim3(256), 0, stream, wb,
-                     ws, sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   const bool vec = (O % 4) == 0 && (I % 4) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&

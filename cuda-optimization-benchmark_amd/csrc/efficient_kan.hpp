@@ -17,12 +17,13 @@
 // x's knot interval, evaluates the four bases nonzero there from per-interval cubic
 // coefficients and shifts them into its 8 slots.
 //
-// Per call: kan_prepare finds each output column's power-of-two scale (so neither fp16
-// half under- or overflows); kan_pack writes the weights ([Wb | Ws*sc], the A operand) in
-// that K order as scaled fp16 hi/lo, [chunk][column][32] so each chunk's tile is contiguous,
-// and tabulates every feature's knot row and per-interval basis cubics; kan_fused is the
-// warp-specialized GEMM (producer waves copy weight tiles and expand activations into LDS,
-// consumer waves run the MFMAs) and undoes the column scale in its epilogue.
+// Per call, two launches: kan_pack finds each output column's power-of-two scale (so
+// neither fp16 half under- or overflows), writes the weights ([Wb | Ws*sc], the A operand)
+// in that K order as scaled fp16 hi/lo, [chunk][column][32] so each chunk's tile is
+// contiguous, and tabulates every feature's knot row and per-interval basis cubics;
+// kan_fused is the warp-specialized GEMM (producer waves copy weight tiles and expand
+// activations into LDS, consumer waves run the MFMAs) and undoes the column scale in its
+// epilogue.
 #pragma once
 
 #include <utility>
@@ -143,8 +144,8 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 }
 
 // ---------------------------------------------------------------------------------------
-// Weight preparation, in two launches: kan_prepare finds each output column's scale,
-// kan_pack writes the GEMM's A operand and builds the basis tables.
+// Weight preparation, one launch (kan_pack): each output column's scale, the GEMM's A
+// operand, and the basis tables.
 // bhi/blo: [nchunks][Opad][32] fp16; chunk q = g*(1+Cp) + sub; sub 0 holds Wb[o, 32g + s],
 // sub >= 1 holds (Ws*sc)[o, f, c] with f = 32g + (s/Cp)*Cp + (sub-1), c = s % Cp (zero
 // past I, O or C), all times 2^e.  So over a group's spline chunks the lanes that supply
@@ -153,58 +154,14 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 // contiguous run.  colscale[o] = 2^-e with e chosen so max|column| * 2^e is in
 // [2^14, 2^15), so neither fp16 half under- or overflows.
 // ---------------------------------------------------------------------------------------
-// kan_prepare: workgroup o reduces column o (contiguous rows of wb, sc and ws) to
-// colscale[o].  Workgroup 0 also zeroes kan_fused's split-K arrival counters (their place in
-// the workspace moves with the shape, so every call starts them from zero).
-__global__ __launch_bounds__(256) void kan_prepare(
-    const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
-    int O, int C, float* __restrict__ colscale, unsigned* __restrict__ counters, int ncounters) {
-  __shared__ float red[4];
-  const int o = blockIdx.x;
-  if (o == 0)
-    for (int i = threadIdx.x; i < ncounters; i += 256) counters[i] = 0u;
-  float mx = 0.0f;
-  if (o < O) {
-    // max_c |ws * s| = |s| * max_c |ws| exactly (rounding is monotonic).  Features are
-    // unrolled four at a time so each thread keeps its loads in flight together.
-    const float* wsc = ws + (size_t)o * I * C;
-    const bool vec = C % 4 == 0 && (reinterpret_cast<uintptr_t>(wsc) & 15) == 0;
-    for (int i0 = threadIdx.x; i0 < I; i0 += 4 * 256) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = i0 + u * 256;
-        if (i < I) {
-          float m = 0.0f;
-          if (vec) {
-            for (int c = 0; c < C; c += 4) {
-              const f32x4 v = *reinterpret_cast<const f32x4*>(wsc + (size_t)i * C + c);
-              m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
-            }
-          } else {
-            for (int c = 0; c < C; ++c) m = fmaxf(m, fabsf(wsc[(size_t)i * C + c]));
-          }
-          mx = fmaxf(mx, fmaxf(fabsf(wb[(size_t)o * I + i]), fabsf(sc[(size_t)o * I + i]) * m));
-        }
-      }
-    }
-  }
-  for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-  if (threadIdx.x % 64 == 0) red[threadIdx.x / 64] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (mx > 0.0f && mx < __builtin_inff()) e = 14 - ilogbf(mx);
-  e = e > 100 ? 100 : (e < -100 ? -100 : e);
-  if (threadIdx.x == 0) colscale[o] = ldexpf(1.0f, -e);
-}
-
 // Basis tables, one thread per table entry (L per feature: the knot row and the L - 1
-// intervals); uflags[block] = 1 when every knot row the block wrote is uniform
-// (kan_knots_uniform), else 0.
+// intervals), kThreadsPerBlock entries per workgroup; uflags[block] = 1 when every knot
+// row the block wrote is uniform (kan_knots_uniform), else 0.
+template <int kThreadsPerBlock>
 __device__ __forceinline__ void kan_tables_block(int block, const float* __restrict__ grid, int I, int L,
                                                  int ngroups, float* __restrict__ tables,
                                                  int* __restrict__ uflags) {
-  const int idx = block * 256 + (int)threadIdx.x;
+  const int idx = block * kThreadsPerBlock + (int)threadIdx.x;
   const int f = idx / L, j = idx % L - 1;
   bool uniform = true;
   if (f < ngroups * kGroup) {
@@ -224,73 +181,170 @@ __device__ __forceinline__ void kan_tables_block(int block, const float* __restr
 }
 
 // kan_pack: the first tblocks workgroups build the basis tables (kan_tables_block); they
-// need nothing from the packing, so they run beside it.  Workgroup tblocks + ct + g *
-// (Opad / 8) writes the 1 + Cp chunks of feature group g for columns 8ct .. 8ct+7; thread
-// (column o, feature fl) writes all of its feature's bases, which
-// form one run of Cp slots (fl / Cp) * Cp .. in spline chunk 1 + fl % Cp, and threads
-// fl < 4 also write silu slots 8 fl .. +7.  A column's 32 threads so read its contiguous
-// ws rows, and the four threads that fill one 64-byte chunk row sit in the same wave.
-constexpr int kPackCols = 8;
+// need nothing from the packing, so they run beside it.  Workgroup tblocks + t owns output
+// columns kPackCols*t .. +kPackCols-1 with kColWaves waves each; wave q of a column takes
+// the runs of 64 features q*64 + 64*kColWaves*j (lane = feature within the run), so a
+// wave's loads cover 64 consecutive features of the column's contiguous rows.  Pass 1
+// reduces the column's max |w| over Wb, sc and Ws to colscale[o] (waves combine through
+// LDS); pass 2 reads the column again (now from the L2 or the Infinity Cache) and writes its
+// hi/lo weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots
+// (fl / Cp) * Cp .. in spline chunk 1 + fl % Cp of group f / 32 (fl = f % 32), and lanes
+// with fl < 4 also write silu slots 8 fl .. +7.  Workgroup tblocks also zeroes kan_fused's
+// split-K arrival counters (their place in the workspace moves with the shape, so every
+// call starts them from zero).
+constexpr int kPackCols = 2;
+constexpr int kColWaves = 4;
+constexpr int kPackThreads = kPackCols * kColWaves * kWave;
 template <int kCp>
-__global__ __launch_bounds__(256) void kan_pack(
+__global__ __launch_bounds__(kPackThreads) void kan_pack(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
-    int O, int C, int Opad, const float* __restrict__ colscale, _Float16* __restrict__ bhi,
+    int O, int C, int Opad, float* __restrict__ colscale, _Float16* __restrict__ bhi,
     _Float16* __restrict__ blo, const float* __restrict__ grid, int L, int ngroups, int tblocks,
-    float* __restrict__ tables, int* __restrict__ uflags) {
-  static_assert(kCp % 8 == 0 && kPackCols * kGroup == 256, "thread per (column, feature)");
+    float* __restrict__ tables, int* __restrict__ uflags, unsigned* __restrict__ counters,
+    int ncounters) {
+  static_assert(kCp % 8 == 0, "whole 8-slot runs");
+  __shared__ float colmax[kPackCols][kColWaves];
   if ((int)blockIdx.x < tblocks) {
-    kan_tables_block(blockIdx.x, grid, I, L, ngroups, tables, uflags);
+    kan_tables_block<kPackThreads>(blockIdx.x, grid, I, L, ngroups, tables, uflags);
     return;
   }
   constexpr int kSub = 1 + kCp;
-  const int b = (int)blockIdx.x - tblocks, ntiles = Opad / kPackCols;
-  const int g = b / ntiles, oc = (int)threadIdx.x / kGroup, fl = (int)threadIdx.x % kGroup;
-  const int o = (b % ntiles) * kPackCols + oc, f = g * kGroup + fl;
-  const float scale = 1.0f / colscale[o];  // 2^e, exact
-  auto put = [&](int sub, int slot, const float* v) {
+  constexpr int kStride = kColWaves * kWave;  // features between a wave's runs
+  const int t = (int)blockIdx.x - tblocks;
+  if (t == 0)
+    for (int i = threadIdx.x; i < ncounters; i += kPackThreads) counters[i] = 0u;
+  const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
+  const int oc = wave / kColWaves, q = wave % kColWaves;
+  const int o = t * kPackCols + oc;
+  const int first = q * kWave + lane;
+  const bool col = o < O;
+  const bool vec = C % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
+  const float* wsc = ws + (size_t)o * I * C;
+  // Ws[o, f, c] for c < kCp (zero past C), times s.
+  auto spline_row = [&](int f, float s, float (&v)[kCp]) {
+    const float* row = wsc + (size_t)f * C;
+    if (vec) {
+#pragma unroll
+      for (int c4 = 0; c4 < kCp / 4; ++c4) {
+        f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
+        if (4 * c4 < C) w4 = *reinterpret_cast<const f32x4*>(row + 4 * c4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * c4 + e] = w4[e] * s;
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < kCp; ++c) v[c] = c < C ? row[c] * s : 0.0f;
+    }
+  };
+
+  // Pass 1: max over the column.  max_c |ws * s| = |s| * max_c |ws| exactly (rounding is
+  // monotonic); a wave's runs go four at a time so each lane keeps its loads in flight.  The
+  // last four runs stay in registers for pass 2.
+  float mx = 0.0f;
+  float wbv[4], scv[4], rows[4][kCp];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    wbv[u] = 0.0f;
+    scv[u] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kCp; ++c) rows[u][c] = 0.0f;
+  }
+  if (col) {
+    for (int f0 = first; f0 < I; f0 += 4 * kStride) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int f = f0 + u * kStride;
+        wbv[u] = 0.0f;
+        scv[u] = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kCp; ++c) rows[u][c] = 0.0f;
+        if (f < I) {
+          wbv[u] = wb[(size_t)o * I + f];
+          scv[u] = sc[(size_t)o * I + f];
+          spline_row(f, 1.0f, rows[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float m = 0.0f;
+#pragma unroll
+        for (int c = 0; c < kCp; ++c) m = fmaxf(m, fabsf(rows[u][c]));
+        mx = fmaxf(mx, fmaxf(fabsf(wbv[u]), fabsf(scv[u]) * m));
+      }
+    }
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+  if (lane == 0) colmax[oc][q] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kColWaves; ++w) mx = fmaxf(mx, colmax[oc][w]);
+  int e = 0;
+  if (mx > 0.0f && mx < __builtin_inff()) e = 14 - ilogbf(mx);
+  e = e > 100 ? 100 : (e < -100 ? -100 : e);
+  if (q == 0 && lane == 0) colscale[o] = ldexpf(1.0f, -e);
+  const float scale = ldexpf(1.0f, e);  // 2^e, exact
+
+  // Pass 2: the scaled hi/lo weights of every group (zero past I and O).
+  auto put = [&](int g, int sub, int slot, const float* v) {
     f16x8 h8, l8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float w = v[e] * scale;
+    for (int k = 0; k < 8; ++k) {
+      const float w = v[k] * scale;
       const _Float16 h = (_Float16)w;
-      h8[e] = h;
-      l8[e] = (_Float16)(w - (float)h);
+      h8[k] = h;
+      l8[k] = (_Float16)(w - (float)h);
     }
     const size_t dst = ((size_t)(g * kSub + sub) * Opad + o) * kChunk + slot;
     *reinterpret_cast<f16x8*>(bhi + dst) = h8;
     *reinterpret_cast<f16x8*>(blo + dst) = l8;
   };
-  float v[kCp];
+  if (ngroups * kGroup <= 4 * kStride) {
+    // One batch of runs covers every feature (I <= 1024): pass 1's registers hold the
+    // column's data.  Lane f % 32 < 4 of a group takes the silu weights of features
+    // 8 (f % 32) .. +7 from the lanes that loaded them (a group sits within one run).
 #pragma unroll
-  for (int c = 0; c < kCp; ++c) v[c] = 0.0f;
-  if (o < O && f < I) {
-    const float s = sc[(size_t)o * I + f];
-    const float* row = ws + ((size_t)o * I + f) * C;
-    if (C % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0) {
+    for (int u = 0; u < 4; ++u) {
+      const int f = first + u * kStride, g = f / kGroup, fl = f % kGroup;
+      float v[kCp], silu[8];
 #pragma unroll
-      for (int c4 = 0; c4 < kCp / 4; ++c4) {
-        if (4 * c4 < C) {
-          const f32x4 q = *reinterpret_cast<const f32x4*>(row + 4 * c4);
+      for (int c = 0; c < kCp; ++c) v[c] = rows[u][c] * scv[u];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[4 * c4 + e] = q[e] * s;
+      for (int k = 0; k < 8; ++k) silu[k] = __shfl(wbv[u], (lane & 32) + ((8 * (lane & 3) + k) & 31), kWave);
+      if (f < ngroups * kGroup) {
+#pragma unroll
+        for (int h = 0; h < kCp / 8; ++h) put(g, 1 + fl % kCp, (fl / kCp) * kCp + 8 * h, v + 8 * h);
+        if (fl < 4) put(g, 0, 8 * fl, silu);
+      }
+    }
+    return;
+  }
+  for (int f0 = first; f0 < ngroups * kGroup; f0 += 2 * kStride) {
+    float rows2[2][kCp], silu[2][8];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int f = f0 + u * kStride, g = f / kGroup, fl = f % kGroup;
+#pragma unroll
+      for (int c = 0; c < kCp; ++c) rows2[u][c] = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) silu[u][k] = 0.0f;
+      if (col && f < I) spline_row(f, sc[(size_t)o * I + f], rows2[u]);
+      if (fl < 4) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const int f2 = g * kGroup + 8 * fl + k;
+          if (col && f2 < I) silu[u][k] = wb[(size_t)o * I + f2];
         }
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < kCp; ++c)
-        if (c < C) v[c] = row[c] * s;
     }
-  }
 #pragma unroll
-  for (int h = 0; h < kCp / 8; ++h) put(1 + fl % kCp, (fl / kCp) * kCp + 8 * h, v + 8 * h);
-  if (fl < 4) {
-    float u[8];
+    for (int u = 0; u < 2; ++u) {
+      const int f = f0 + u * kStride, g = f / kGroup, fl = f % kGroup;
+      if (f < ngroups * kGroup) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int f2 = g * kGroup + 8 * fl + e;
-      u[e] = o < O && f2 < I ? wb[(size_t)o * I + f2] : 0.0f;
+        for (int h = 0; h < kCp / 8; ++h) put(g, 1 + fl % kCp, (fl / kCp) * kCp + 8 * h, rows2[u] + 8 * h);
+        if (fl < 4) put(g, 0, 8 * fl, silu[u]);
+      }
     }
-    put(0, 8 * fl, u);
   }
 }
 

@@ -4,7 +4,7 @@
         Per-kernel dispatch count and average / median / min / max duration from a
         `rocprofv3 --kernel-trace --stats -d DIR` run (a markdown table).
 
-    python cuda-optimization-benchmark_amd/profiling.py mfma DIR [--simds 1024] [--xcds 8]
+    python cuda-optimization-benchmark_amd/profiling.py mfma DIR [--simds 1024] [--xcds 8] [--json OUT]
         MFMA utilisation per kernel from a `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES
         SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_VALU_MFMA_MOPS_F8 GRBM_GUI_ACTIVE` run:
         busy = MFMA-busy cycles summed over SIMDs / (GUI-active cycles x SIMDs), the
@@ -18,7 +18,8 @@
         `--pmc WRITE_SIZE` runs of `bench.py --copy-probe`.  Both counters (KiB per
         dispatch) are scaled by what they read for the probe's plain device copy of
         bench.COPY_PROBE_BYTES, so a copy of n bytes reads exactly n fetched and n written.
-        With --json, writes {bench op key: bytes per launch of its dominant kernel}.
+        With --json, writes {"values": {bench op key: bytes per launch of its dominant
+        kernel}, "call_values": {op: bytes per call, every kernel}, "source", "commit"}.
 
 Only the standard library is used: the databases are SQLite files.
 """
@@ -45,6 +46,11 @@ DOMINANT = {
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny_flat",
     "quantize_e4m3": "qz_fused",
+}
+# Every kernel one call launches, for the ops that launch more than one; their traffic is
+# summed into the call's total.
+CALL_KERNELS = {
+    "efficient_kan": ("kan_pack", "kan_fused"),
 }
 COPY_PROBE_BYTES = 256 << 20
 
@@ -134,9 +140,9 @@ def print_traffic(t: dict) -> None:
         print(f"| `{_short(k)}` | {r['dispatches']} | {fb / 1e6:.2f} | {wb / 1e6:.2f} | {(fb + wb) / 1e6:.2f} |")
 
 
-def dominant_traffic(t: dict) -> dict:
+def dominant_traffic(t: dict, table: dict = DOMINANT) -> dict:
     out = {}
-    for op, subs in DOMINANT.items():
+    for op, subs in table.items():
         total, found = 0.0, True
         for sub in (subs,) if isinstance(subs, str) else subs:
             hits = [r for k, r in t["kernels"].items() if sub in k and "copy" not in k.lower()]
@@ -179,6 +185,15 @@ def print_mfma(u: dict) -> None:
         print(f"| `{_short(k)}` | {r['dispatches']} | {r['busy_pct']:.1f} | {r['f16_flop']:.4g} | {r['f8_flop']:.4g} |")
 
 
+def _write_json(path: str, body: dict, a) -> None:
+    """The summary bench.py reads: the figures plus where they came from (the profiles/
+    file that shows them and the commit of the profiled build)."""
+    body = dict(body, source=a.source, commit=a.commit)
+    with open(path, "w") as fh:
+        json.dump(body, fh, indent=1, sort_keys=True)
+        fh.write("\n")
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -193,6 +208,9 @@ def main(argv=None) -> int:
     t.add_argument("fetch_dir")
     t.add_argument("write_dir")
     t.add_argument("--json")
+    for p in (m, t):
+        p.add_argument("--commit", default="", help="the source commit the profiled build came from")
+        p.add_argument("--source", default="", help="the profiles/ summary these figures appear in")
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print_stats(a.dir)
@@ -205,16 +223,13 @@ def main(argv=None) -> int:
                 hits = [r["busy_pct"] for k, r in u.items() if isinstance(sub, str) and sub in k]
                 if hits:
                     dom[op] = round(statistics.mean(hits), 1)
-            with open(a.json, "w") as fh:
-                json.dump(dom, fh, indent=1, sort_keys=True)
-                fh.write("\n")
+            _write_json(a.json, {"values": dom}, a)
     else:
         tr = traffic(a.fetch_dir, a.write_dir)
         print_traffic(tr)
         if a.json:
-            with open(a.json, "w") as fh:
-                json.dump(dominant_traffic(tr), fh, indent=1, sort_keys=True)
-                fh.write("\n")
+            _write_json(a.json, {"values": dominant_traffic(tr),
+                                 "call_values": dominant_traffic(tr, CALL_KERNELS)}, a)
     return 0
 
 

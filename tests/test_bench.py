@@ -100,3 +100,29 @@ def test_json_line_on_gpu():
     assert abs(roof["frac"] - roof["achieved"] / roof["peak"]) < 1e-3
     cpu = d["cpu_baseline"]
     assert cpu["value"] > 0 and cpu["unit"] == "us/call" and cpu["cores"] >= 1 and cpu["kind"] == "port"
+
+
+def test_profile_summaries_name_their_source():
+    """traffic.json and mfma.json carry the figures bench.py copies into the roofline, with
+    the profiles/ file and commit they came from; bench tags each copied figure with that."""
+    for name in ("traffic.json", "mfma.json"):
+        s = bench._profile_json(name)
+        assert set(s) >= {"values", "source", "commit"}, name
+        assert s["source"].startswith("profiles/") and (ROOT / s["source"]).exists()
+        assert len(s["commit"]) >= 7
+        note = bench._provenance(s, name)
+        assert s["commit"] in note and "not measured by this run" in note
+    t = bench._profile_json("traffic.json")
+    assert set(t["values"]) <= set(bench.WORKLOADS)
+    assert "efficient_kan" in t["call_values"]
+    assert t["call_values"]["efficient_kan"] >= t["values"]["efficient_kan"]
+
+
+def test_profiling_json_writer(tmp_path):
+    """profiling.py's summary writer: the figures plus source and commit."""
+    import json
+    from types import SimpleNamespace
+    from cob_amd import profiling
+    out = tmp_path / "x.json"
+    profiling._write_json(str(out), {"values": {"leaky": 1}}, SimpleNamespace(source="profiles/a.md", commit="abc1234"))
+    assert json.loads(out.read_text()) == {"values": {"leaky": 1}, "source": "profiles/a.md", "commit": "abc1234"}

@@ -118,6 +118,10 @@ KAN_SHAPES = [
     # 96 tiles, ragged O and 3 groups split 2+1.
     (4096, 160, 512, 8, 3, 1.0, "uniform"),
     (4096, 90, 600, 5, 3, 1.0, "random"),
+    # More than 1024 features: the weight packing reads each column twice instead of
+    # keeping one batch of runs in registers (both padded basis widths).
+    (24, 1100, 40, 5, 3, 1.0, "uniform"),
+    (20, 1030, 33, 10, 3, 1.0, "random"),
 ]
 
 
