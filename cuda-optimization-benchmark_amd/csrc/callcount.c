@@ -91,29 +91,47 @@ static void* resolve(const char* name) {
     return e_;                      \
   } while (0)
 
-/* Copy kind: 1 when host memory is involved.  hipMemcpyDefault asks the runtime where
- * each pointer lives; memory the runtime does not know is host memory. */
-static int touches_host(hipMemcpyKind k, const void* dst, const void* src) {
-  if (k == hipMemcpyDeviceToDevice) return 0;
-  if (k != hipMemcpyDefault) return 1;
+/* ---- where the two ends of a copy live ----
+ * A copy is a host copy when either end is host memory.  An explicit kind names both ends;
+ * hipMemcpyDefault (and any kind this file does not know) asks the runtime about each
+ * pointer, and memory the runtime does not know counts as host memory. */
+enum copy_end { END_HOST, END_DEVICE };
+
+static enum copy_end locate(const void* p) {
   static __typeof__(&hipPointerGetAttributes) attrs;
   if (!attrs) attrs = (__typeof__(&hipPointerGetAttributes))resolve("hipPointerGetAttributes");
-  if (!attrs) return 1;
-  const void* p[2] = {dst, src};
-  for (int i = 0; i < 2; ++i) {
-    hipPointerAttribute_t a;
-    memset(&a, 0, sizeof a);
-    ++t_depth;
-    const hipError_t e = attrs(&a, p[i]);
-    --t_depth;
-    if (e != hipSuccess || (a.type != hipMemoryTypeDevice && a.type != hipMemoryTypeManaged)) return 1;
+  if (!attrs) return END_HOST;
+  hipPointerAttribute_t a;
+  memset(&a, 0, sizeof a);
+  ++t_depth;
+  const hipError_t e = attrs(&a, p);
+  --t_depth;
+  if (e != hipSuccess) return END_HOST;
+  return (a.type == hipMemoryTypeDevice || a.type == hipMemoryTypeManaged) ? END_DEVICE : END_HOST;
+}
+
+/* Ends of a copy from `src` to `dst`; a NULL pointer is an end known to be device memory
+ * (a symbol), located only when the kind does not say. */
+static void copy_ends(hipMemcpyKind k, const void* dst, const void* src, enum copy_end* from,
+                      enum copy_end* to) {
+  switch (k) {
+    case hipMemcpyHostToHost: *from = END_HOST; *to = END_HOST; return;
+    case hipMemcpyHostToDevice: *from = END_HOST; *to = END_DEVICE; return;
+    case hipMemcpyDeviceToHost: *from = END_DEVICE; *to = END_HOST; return;
+    case hipMemcpyDeviceToDevice:
+    case hipMemcpyDeviceToDeviceNoCU: *from = END_DEVICE; *to = END_DEVICE; return;
+    default:
+      *from = src ? locate(src) : END_DEVICE;
+      *to = dst ? locate(dst) : END_DEVICE;
+      return;
   }
-  return 0;
 }
 
 /* A copy on stream s (synchronous copies run on the null stream). */
 static void note_copy(hipMemcpyKind k, const void* dst, const void* src, hipStream_t s) {
-  if (touches_host(k, dst, src))
+  enum copy_end from, to;
+  copy_ends(k, dst, src, &from, &to);
+  if (from == END_HOST || to == END_HOST)
     note(CC_HOST_COPY);
   else
     note_on(CC_DEVICE_COPY, s);
@@ -167,28 +185,20 @@ hipError_t hipMemcpy2DAsync(void* d, size_t dp, const void* s, size_t sp, size_t
                             hipStream_t st) {
   RESOLVE(hipMemcpy2DAsync); note_copy(k, d, s, st); FORWARD(d, dp, s, sp, w, h, k, st);
 }
-/* Symbol copies: the symbol is device memory, the other side is host unless D2D. */
+/* Symbol copies: the symbol end is device memory (passed as NULL to note_copy). */
 hipError_t hipMemcpyToSymbol(const void* sym, const void* s, size_t n, size_t off, hipMemcpyKind k) {
-  RESOLVE(hipMemcpyToSymbol);
-  if (k == hipMemcpyDeviceToDevice) note_on(CC_DEVICE_COPY, NULL); else note(CC_HOST_COPY);
-  FORWARD(sym, s, n, off, k);
+  RESOLVE(hipMemcpyToSymbol); note_copy(k, NULL, s, NULL); FORWARD(sym, s, n, off, k);
 }
 hipError_t hipMemcpyToSymbolAsync(const void* sym, const void* s, size_t n, size_t off, hipMemcpyKind k,
                                   hipStream_t st) {
-  RESOLVE(hipMemcpyToSymbolAsync);
-  if (k == hipMemcpyDeviceToDevice) note_on(CC_DEVICE_COPY, st); else note(CC_HOST_COPY);
-  FORWARD(sym, s, n, off, k, st);
+  RESOLVE(hipMemcpyToSymbolAsync); note_copy(k, NULL, s, st); FORWARD(sym, s, n, off, k, st);
 }
 hipError_t hipMemcpyFromSymbol(void* d, const void* sym, size_t n, size_t off, hipMemcpyKind k) {
-  RESOLVE(hipMemcpyFromSymbol);
-  if (k == hipMemcpyDeviceToDevice) note_on(CC_DEVICE_COPY, NULL); else note(CC_HOST_COPY);
-  FORWARD(d, sym, n, off, k);
+  RESOLVE(hipMemcpyFromSymbol); note_copy(k, d, NULL, NULL); FORWARD(d, sym, n, off, k);
 }
 hipError_t hipMemcpyFromSymbolAsync(void* d, const void* sym, size_t n, size_t off, hipMemcpyKind k,
                                     hipStream_t st) {
-  RESOLVE(hipMemcpyFromSymbolAsync);
-  if (k == hipMemcpyDeviceToDevice) note_on(CC_DEVICE_COPY, st); else note(CC_HOST_COPY);
-  FORWARD(d, sym, n, off, k, st);
+  RESOLVE(hipMemcpyFromSymbolAsync); note_copy(k, d, NULL, st); FORWARD(d, sym, n, off, k, st);
 }
 
 /* ---- memsets (synchronous ones run on the null stream) ---- */
