@@ -49,8 +49,8 @@ constexpr unsigned kOutOfRange = 0x80000000u;
 // kan_fused tiling: a 128 x 256 output tile per workgroup of 8 waves.  Waves 0-3 are
 // consumers: wave w owns all 128 batch rows (8 row blocks of 16) x output columns
 // 64w .. 64w+63 (4 column blocks), 128 fp32 accumulators, and only reads LDS and issues
-// MFMAs.  Waves 4-7 are producers: producer p copies a quarter of each weight tile into
-// LDS and expands the activations of batch rows 32p .. 32p+31 (2 row blocks).  One
+// MFMAs.  Waves 4-7 are producers: producer p copies a quarter of each weight half-tile
+// into LDS and expands the activations of batch rows 32p .. 32p+31 (2 row blocks).  One
 // producer and one consumer share each SIMD.
 constexpr int kThreads = 512;
 constexpr int kConsumerWaves = 4;
@@ -58,15 +58,18 @@ constexpr int BM = 128;
 constexpr int BN = 256;
 constexpr int kRB = BM / 16;                        // row blocks per tile (consumer)
 constexpr int kCB = BN / 16 / kConsumerWaves;       // column blocks per consumer wave
-constexpr int kWHalfBytes = BN * kChunk * 2;        // hi or lo weights of one chunk: 16 KiB
-constexpr int kWStageBytes = 2 * kWHalfBytes;       // one chunk's weight tile: 32 KiB
-constexpr int kWStages = 3;                         // weight ring: copies run two chunks ahead
-constexpr int kActBytes = kRB * 2 * 64 * 16;        // hi + lo activation fragments: 16 KiB
+constexpr int kSubTileBytes = BN * kChunk * 2;      // one plane (hi or lo) of one 32-k chunk: 16 KiB
+constexpr int kSlotBytes = 2 * kSubTileBytes;       // a half-tile: one plane of a 64-k step
+constexpr int kSlots = 3;                           // half-tile ring
+constexpr int kActFragBytes = kRB * 2 * 64 * 16;    // hi + lo activation fragments: 16 KiB
+constexpr int kActIdxBytes = kRB * 64 * 4;          // sparse positions: 2 KiB
+constexpr int kActBytes = kActFragBytes + kActIdxBytes;
 constexpr int kActStages = 2;
-constexpr int kActAt = kWStages * kWStageBytes;
+constexpr int kActAt = kSlots * kSlotBytes;
 constexpr int kTblAt = kActAt + kActStages * kActBytes;
-constexpr int kTblBytes = 32 * 1024;                // one group's table (L <= 16)
-constexpr int kLdsBytes = kTblAt + kTblBytes;       // 160 KiB
+constexpr int kTblSetSlots = 8;                     // features per table set (C' = 8; C' = 16 uses 4)
+constexpr int kTblBytes = 2 * kTblSetSlots * 64 * kMaxKnots;  // two sets of 1 KiB entries: 16 KiB
+constexpr int kLdsBytes = kTblAt + kTblBytes;       // 148 KiB
 static_assert(kLdsBytes <= 160 * 1024, "fits one CU's LDS");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, size_t bytes) {
@@ -154,6 +157,30 @@ __host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, i
 // contiguous run.  colscale[o] = 2^-e with e chosen so max|column| * 2^e is in
 // [2^14, 2^15), so neither fp16 half under- or overflows.
 // ---------------------------------------------------------------------------------------
+// The GEMM's K order within a feature group (32 features): chunk 0 holds silu(x) of the 32
+// features (k = feature); chunks 1 .. C' hold the spline bases, in C'/2 steps of 64 k (two
+// chunks each) that the sparse MFMA consumes whole.  In step u, lane quarter q of the MFMA
+// supplies k = 16 q .. 16 q + 15 of the step:
+//   C' = 8:  features 8q + 2u and 8q + 2u + 1, 8 slots each, bases in the order 0 2 4 6 1 3 5 7;
+//   C' = 16: feature 8q + u, 16 slots, bases in the order 0 4 8 12 1 5 9 13 2 6 10 14 3 7 11 15.
+// Each group of 4 slots then holds at most two of a feature's four nonzero bases (the
+// window j-3 .. j has two even and two odd bases, and one basis per residue mod 4), the
+// 2:4 pattern of v_smfmac_f32_16x16x64_f16.  Over a group a lane quarter's features are the
+// contiguous run 8q .. 8q + 7.
+template <int kCp>
+__host__ __device__ inline void spline_k(int fl, int& sub, int& slot) {
+  const int q = fl / 8;
+  const int u = kCp == 8 ? (fl % 8) / 2 : fl % 8;
+  const int k = kCp == 8 ? 16 * q + 8 * (fl % 2) : 16 * q;  // first k of the feature's slots in its step
+  sub = 1 + 2 * u + k / 32;
+  slot = k % 32;
+}
+// Basis in slot s of a feature's C' slots.
+template <int kCp>
+__host__ __device__ constexpr int spline_basis(int s) {
+  return kCp == 8 ? (s < 4 ? 2 * s : 2 * (s - 4) + 1) : 4 * (s % 4) + s / 4;
+}
+
 // Basis tables, one thread per table entry (L per feature: the knot row and the L - 1
 // intervals), kThreadsPerBlock entries per workgroup; uflags[block] = 1 when every knot
 // row the block wrote is uniform (kan_knots_uniform), else 0.
@@ -298,6 +325,17 @@ __global__ __launch_bounds__(kPackThreads) void kan_pack(
     *reinterpret_cast<f16x8*>(bhi + dst) = h8;
     *reinterpret_cast<f16x8*>(blo + dst) = l8;
   };
+  // Feature fl's bases in the GEMM's sparse K order (spline_k): one run of C' slots, the
+  // bases permuted so every group of 4 slots holds at most two of the four nonzero ones.
+  auto put_spline = [&](int g, int fl, const float (&v)[kCp]) {
+    int sub, slot;
+    spline_k<kCp>(fl, sub, slot);
+    float w[kCp];
+#pragma unroll
+    for (int s = 0; s < kCp; ++s) w[s] = v[spline_basis<kCp>(s)];
+#pragma unroll
+    for (int h = 0; h < kCp / 8; ++h) put(g, sub, slot + 8 * h, w + 8 * h);
+  };
   if (ngroups * kGroup <= 4 * kStride) {
     // One batch of runs covers every feature (I <= 1024): pass 1's registers hold the
     // column's data.  Lane f % 32 < 4 of a group takes the silu weights of features
@@ -311,8 +349,7 @@ __global__ __launch_bounds__(kPackThreads) void kan_pack(
 #pragma unroll
       for (int k = 0; k < 8; ++k) silu[k] = __shfl(wbv[u], (lane & 32) + ((8 * (lane & 3) + k) & 31), kWave);
       if (f < ngroups * kGroup) {
-#pragma unroll
-        for (int h = 0; h < kCp / 8; ++h) put(g, 1 + fl % kCp, (fl / kCp) * kCp + 8 * h, v + 8 * h);
+        put_spline(g, fl, v);
         if (fl < 4) put(g, 0, 8 * fl, silu);
       }
     }
@@ -340,8 +377,7 @@ __global__ __launch_bounds__(kPackThreads) void kan_pack(
     for (int u = 0; u < 2; ++u) {
       const int f = f0 + u * kStride, g = f / kGroup, fl = f % kGroup;
       if (f < ngroups * kGroup) {
-#pragma unroll
-        for (int h = 0; h < kCp / 8; ++h) put(g, 1 + fl % kCp, (fl / kCp) * kCp + 8 * h, rows2[u] + 8 * h);
+        put_spline(g, fl, rows2[u]);
         if (fl < 4) put(g, 0, 8 * fl, silu[u]);
       }
     }
@@ -447,162 +483,155 @@ __device__ __forceinline__ TabFetch tab_locate_uniform(float x, float t0, float 
   return r;
 }
 
-// Evaluates the four cubics at u = x - t_j, splits them into fp16 hi/lo and routes them to
-// the lane's 8 slots (bases b0 .. b0+7).  Basis c sits in slot c - b0; the value of
-// coefficient chunk m belongs to the one basis of the window [j-3, j] with index = m
-// (mod 4), so it goes to slot m or m + 4 (b0 is a multiple of 8), or to neither when that
-// basis belongs to the other lane (Cp = 16).  With Cp = 8 (b0 = 0) bases outside [0, 8)
-// have zero coefficients, so only the routing is needed: chunk m goes to slot m + 4
-// exactly when m < j - 3.
-template <int kCp>
-__device__ __forceinline__ void tab_finish(float x, const TabFetch& t, int b0, f16x8& hi, f16x8& lo) {
+// The four cubics at u = x - t_j: N[m] is the basis of the window [j-3, j] with index = m
+// (mod 4); zero outside the knot span, and the table holds zero coefficients for bases
+// outside [0, C).
+__device__ __forceinline__ void tab_values(float x, const TabFetch& t, float (&N)[4]) {
   const float u = x - t.tj;
-  float N[4];
 #pragma unroll
   for (int m = 0; m < 4; ++m) {
     const f32x4 c = t.c[m];
     N[m] = t.inside ? fmaf(fmaf(fmaf(c.w, u, c.z), u, c.y), u, c.x) : 0.0f;
   }
-  asm volatile("" : "+v"(N[0]), "+v"(N[1]), "+v"(N[2]), "+v"(N[3]));
-  const f16x2 h01 = __builtin_convertvector(f32x2{N[0], N[1]}, f16x2);
-  const f16x2 h23 = __builtin_convertvector(f32x2{N[2], N[3]}, f16x2);
-  // lo = fp16(N - hi), the difference exact in fp32: one v_fma_mix per value.
-  f16x2 l01, l23;
-  l01.x = (_Float16)__builtin_fmaf((float)h01.x, -1.0f, N[0]);
-  l01.y = (_Float16)__builtin_fmaf((float)h01.y, -1.0f, N[1]);
-  l23.x = (_Float16)__builtin_fmaf((float)h23.x, -1.0f, N[2]);
-  l23.y = (_Float16)__builtin_fmaf((float)h23.y, -1.0f, N[3]);
-  const unsigned H0 = __builtin_bit_cast(unsigned, h01), H1 = __builtin_bit_cast(unsigned, h23);
-  const unsigned L0 = __builtin_bit_cast(unsigned, l01), L1 = __builtin_bit_cast(unsigned, l23);
-  unsigned m0, m1, m2, m3;  // slot masks: slots 2d, 2d+1 take fp16 halves of dword d % 2
-  if constexpr (kCp == 8) {
-    const int k = min(max(t.j - kOrder, 0), 4);  // chunks m < k go to slots m + 4
-    const unsigned long long M = k < 4 ? (~0ull << (16 * k)) : 0ull;
-    m0 = (unsigned)M;
-    m1 = (unsigned)(M >> 32);
-    m2 = ~m0;
-    m3 = ~m1;
-  } else {
-    // Slot s is live iff s in [p, p+3], p = j - 3 - b0 in [-11, 11]: bit s of `act`.
-    const int p = t.j - kOrder - b0;
-    const unsigned act = (0xFu << (p + 11)) >> 11;
-    auto pair = [&](int s) {
-      return (__builtin_amdgcn_sbfe(act, s, 1) & 0xFFFFu) | (__builtin_amdgcn_sbfe(act, s + 1, 1) & 0xFFFF0000u);
-    };
-    m0 = pair(0);
-    m1 = pair(2);
-    m2 = pair(4);
-    m3 = pair(6);
-  }
-  hi = __builtin_bit_cast(f16x8, i32x4{(int)(H0 & m0), (int)(H1 & m1), (int)(H0 & m2), (int)(H1 & m3)});
-  lo = __builtin_bit_cast(f16x8, i32x4{(int)(L0 & m0), (int)(L1 & m1), (int)(L0 & m2), (int)(L1 & m3)});
 }
 
-// kVec: O and I multiples of 4 and out, x 16-byte aligned (16-byte output stores and x
-// loads); otherwise 4-byte ones.  kUniform: every knot row passed kan_knots_uniform.
-//
-// Split-K (nsplit > 1, for grids of fewer tiles than CUs): workgroup b computes split
-// b % nsplit, feature groups [split*gper, split*gper + gper), of tile b / nsplit.  It
-// writes its fp32 partial tile to `partial` and arrives on the tile's counter; the last
-// of the tile's nsplit arrivals sums the partials in split order (so the result does not
+// Two bases at consecutive positions first, first + 1 of a group of 4 slots (values v0, v1)
+// as a sparse pair: the positions clamped into the group (a pair past its ends holds bases
+// outside [0, C'), whose values are zero) and the values that land on them.
+__device__ __forceinline__ void sparse_pair(int first, float v0, float v1, float& a, float& b, unsigned& pos) {
+  const int p = min(max(first, 0), 2);
+  const int d = p - first;  // 1, 0, -1 or -2
+  a = d == 0 ? v0 : (d == 1 ? v1 : 0.0f);
+  b = d == 0 ? v1 : (d == -1 ? v0 : 0.0f);
+  pos = (unsigned)p | ((unsigned)(p + 1) << 2);
+}
+
+// One feature's compressed A values for C' = 8 (4 values: group 0 the even bases, group 1
+// the odd ones) and their 8 position bits.
+__device__ __forceinline__ void sparse8(int j, const float (&N)[4], float* v, unsigned& bits) {
+  const int e0 = (j & 1) ? j - 3 : j - 2;  // the window's first even basis
+  const int o0 = (j & 1) ? j - 2 : j - 3;  // and first odd one
+  // N[m] holds the basis = m (mod 4): e0 and e0 + 2 are 0 and 2 (mod 4) in some order
+  const bool es = (e0 & 2) != 0, os = (o0 & 2) != 0;
+  unsigned pe, po;
+  sparse_pair(e0 >> 1, es ? N[2] : N[0], es ? N[0] : N[2], v[0], v[1], pe);
+  sparse_pair((o0 - 1) >> 1, os ? N[3] : N[1], os ? N[1] : N[3], v[2], v[3], po);
+  bits = pe | (po << 4);
+}
+
+// One feature's compressed A values for C' = 16 (8 values: group r the bases = r (mod 4),
+// one of them nonzero, paired with a zero at the neighbouring position) and 16 position bits.
+__device__ __forceinline__ void sparse16(int j, const float (&N)[4], float* v, unsigned& bits) {
+  bits = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int b = j - 3 + ((r - (j - 3)) & 3);  // the window's basis = r (mod 4)
+    const int pos = b >> 2;                     // its position in group r (-1: no such basis)
+    const int p = pos < 0 ? 0 : (pos & ~1);
+    const bool odd = pos >= 0 && (pos & 1);
+    v[2 * r] = odd ? 0.0f : N[r];
+    v[2 * r + 1] = odd ? N[r] : 0.0f;
+    bits |= ((unsigned)p | ((unsigned)(p + 1) << 2)) << (4 * r);
+  }
+}
+
+// kVec: O and I multiples of 4 and out, x 16-byte aligned (16-byte x loads); otherwise
+// 4-byte ones.  kUniform: every knot row passed kan_knots_uniform.
 
 // ---------------------------------------------------------------------------------------
-// kan_fused: the warp-specialized GEMM.
+// kan_fused: the warp-specialized GEMM over the 2:4-sparse spline activations.
 //
-// LDS (kLdsBytes):
-//   weight ring, 3 x 32 KiB: hi then lo, 256 rows (output columns of the tile) x 64 B
-//     (32 k) each, swizzle64
-//   activation fragments, 2 x 16 KiB: [row block 0..7][hi, lo][lane] x 16 B, exactly the B
-//     operand a consumer lane feeds its MFMA (one conflict-free 16-byte read)
-//   the basis table of the groups in use, 32 KiB
+// Steps: per feature group, step 0 is the silu chunk (32 k, dense v_mfma_f32_16x16x32_f16)
+// and steps 1 .. C'/2 are the spline steps of 64 k (v_smfmac_f32_16x16x64_f16, the
+// activations the sparse A operand: 8 stored values per lane with 2-bit positions, the
+// weights the dense B operand).  The activations are the A operand of both kinds, so a
+// consumer lane's accumulator holds output column n0 + 64 w + 16 cb + lane % 16 of batch
+// rows m0 + 16 rb + 4 (lane / 16) + 0..3.
 //
-// Chunk c of the workgroup's range is computed by the consumers from weight stage c % 3 and
-// activation stage c % 2 while the producers write chunk c + 1's activations (evaluated in
-// registers) and copy chunk c + 2's weight tile (direct-to-LDS), so copies have two chunks
-// to land.  One workgroup barrier per chunk hands the stages over.  x is loaded one group
-// ahead.  Spline chunk t of a group reads the table entries of its own features only (the
-// features xb + t of the lanes), so once a chunk has been prepared its features' entries
-// are refilled with the next group's, a step later.
+// Each product is hi*hi + lo*hi + hi*lo; a step is consumed in two phases: L (hi_a * lo_w)
+// then H (hi_a * hi_w, lo_a * hi_w), so a step's lo and hi weight planes are separate
+// half-tiles in a ring of three 32 KiB slots: half-tile 2s (lo of step s) and 2s + 1 (hi)
+// sit in slot (2s) % 3 and (2s + 1) % 3.  Barriers: A(s) before phase L of step s, B(s)
+// before its phase H.
+//   producers, between A(s) and B(s): copy lo(s+1) into the slot hi(s-1) left, refill the
+//     table set step s's features used, load the next group's x (at a group's silu step),
+//     evaluate row block 0 of step s+1's activations; wait for hi(s);
+//   between B(s) and A(s+1): copy hi(s+1) into the slot lo(s) left, evaluate row block 1,
+//     wait for lo(s+1) (and the table and x loads).
+// Every copy has about one step to land.
+//
+// LDS (kLdsBytes): the ring (3 x 32 KiB: a half-tile is two 16 KiB sub-tiles, the chunks
+// 2u+1 and 2u+2 of spline step u, 256 rows x 64 B each, swizzle64; the silu step uses one);
+// 2 activation stages of 18 KiB ([row block][hi, lo][lane] x 16 B, then the positions
+// [row block][lane] x 4 B); and the basis-table window, two sets of 8 (C' = 8) or 4
+// (C' = 16) feature entries: spline step u's features in set u % 2.
 // ---------------------------------------------------------------------------------------
-// Chunk c's weight tile (rows n0 .. n0 + 255 of [q][Opad][32], hi and lo) into weight stage
-// c % 3: one of the four copying waves (part) copies the 16-row groups 4 part .. 4 part + 3
-// of each half.  A direct-to-LDS instruction writes 64 consecutive 16-byte slots (16 rows of
-// 64 bytes); lane i fetches the chunk the swizzle places in slot i.  kPieces splits the 8
-// copy instructions so a caller can interleave them with other work.
-constexpr int kWeightCopies = 2 * (BN / 16) / 4;  // 1 KiB copies per copying wave per chunk
-template <int kPiece, int kPieces>
-__device__ __forceinline__ void copy_weight_tile(uint8_t* smem, __amdgpu_buffer_rsrc_t rhi, __amdgpu_buffer_rsrc_t rlo,
-                                                 int q, int c, int Opad, int n0, int part, int lane) {
-  uint8_t* st = smem + (c % kWStages) * kWStageBytes;
+
+// Half-tile plane `rp` of the step whose first chunk is q (one sub-tile, or two for a spline
+// step) into ring slot `slot`: copying wave `part` copies the 16-row groups 4 part ..
+// 4 part + 3 of each sub-tile.  A direct-to-LDS instruction writes 64 consecutive 16-byte
+// slots (16 rows of 64 bytes); lane i fetches the chunk the swizzle places in slot i.
+constexpr int kSubTileCopies = BN / 16 / 4;  // 1 KiB copies per copying wave per sub-tile
+template <int kSub>
+__device__ __forceinline__ void copy_half_tile(uint8_t* smem, __amdgpu_buffer_rsrc_t rp, int slot, int q, int Opad,
+                                               int n0, int part, int lane) {
+  uint8_t* st = smem + slot * kSlotBytes;
   const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
-  constexpr int kPer = kWeightCopies / 2 / kPieces;
 #pragma unroll
-  for (int i = kPiece * kPer; i < (kPiece + 1) * kPer; ++i) {
-    const int group = part * (kWeightCopies / 2) + i;
-    const unsigned off = (unsigned)(((size_t)q * Opad + n0 + group * 16 + r16) * 64 + 16 * logical);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rhi, (__attribute__((address_space(3))) void*)(st + group * 1024), 16, off, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        rlo, (__attribute__((address_space(3))) void*)(st + kWHalfBytes + group * 1024), 16, off, 0, 0, 0);
-  }
+  for (int t = 0; t < kSub; ++t)
+#pragma unroll
+    for (int i = 0; i < kSubTileCopies; ++i) {
+      const int group = part * kSubTileCopies + i;
+      const unsigned off = (unsigned)(((size_t)(q + t) * Opad + n0 + group * 16 + r16) * 64 + 16 * logical);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rp, (__attribute__((address_space(3))) void*)(st + t * kSubTileBytes + group * 1024), 16, off, 0, 0, 0);
+    }
 }
 
 template <int kCp, bool kVec>
 struct Producer {
-  static constexpr int kQ = 1 + kCp;
-  static constexpr int kX = kCp;                                    // x values per row block per group
-  static constexpr int kCopies = kWeightCopies;
-  static constexpr int kTableCopies = kTblBytes / 1024 / 4;         // 1 KiB table copies per producer wave
-  static constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;       // x load instructions per group
-  static_assert(2 * kCopies + kTableCopies + kXLoads + 1 <= 63, "vmcnt holds at most 63");
+  static constexpr int kS = kCp / 2;                       // spline steps per group
+  static constexpr int kQ = 1 + kS;                        // steps per group
+  static constexpr int kChunksPerGroup = 1 + kCp;
+  static constexpr int kX = 8;                             // x values per row block per group
+  static constexpr int kSetFeat = kCp == 8 ? 8 : 4;        // features per table set
+  static constexpr int kTableCopies = kSetFeat / 4;        // per producer wave per set
+  static constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;
 
   uint8_t* smem;
   __amdgpu_buffer_rsrc_t rhi, rlo, rx, rt;
-
-  __device__ __forceinline__ void copy_weights(int c) const {
-    copy_weight_tile<0, 1>(smem, rhi, rlo, (g0 + c / kQ) * kQ + c % kQ, c, Opad, n0, pw, lane);
-  }
-
-  // Piece kPiece of 4 of chunk c's weight copies (none past the last chunk).
-  template <int kPiece>
-  __device__ __forceinline__ void copy_weights_piece(int c) const {
-    if (c < nchunks) copy_weight_tile<kPiece, 4>(smem, rhi, rlo, (g0 + c / kQ) * kQ + c % kQ, c, Opad, n0, pw, lane);
-    __builtin_amdgcn_sched_barrier(0);
-  }
   int I, L, B, Opad, n0;
-  int g0, nlg, nchunks;
-  int lane, fr, fg, pw, xb;
+  int g0, nlg;
+  int lane, fr, fq, pw;
   int row[2];      // this lane's batch rows (global) for its two row blocks
   bool uniform;    // every knot row is uniform: direct interval lookup
   int tgb;
 
-  // Group lg's whole table into the table buffer: producer wave pw copies 1 KiB blocks
-  // kTableCopies * pw .. +kTableCopies - 1; blocks past the group's table zero-fill.
-  __device__ __forceinline__ void copy_table(int lg) const {
-    uint8_t* dst = smem + kTblAt;
-    const int g = g0 + lg;
+  // Half-tiles of step s = lg * kQ + j (j = 0: silu, one sub-tile).
+  template <int kJ>
+  __device__ __forceinline__ void copy_step_plane(__amdgpu_buffer_rsrc_t rp, int lg, int slot) const {
+    const int q = (g0 + lg) * kChunksPerGroup + (kJ == 0 ? 0 : 2 * kJ - 1);
+    copy_half_tile<kJ == 0 ? 1 : 2>(smem, rp, slot, q, Opad, n0, pw, lane);
+  }
+
+  // The table entries of spline step u's features of group lg into set u % 2: this wave
+  // copies the features of slots kTableCopies * pw ..; a feature's 64 L bytes are 4 L lanes
+  // of one direct-to-LDS instruction.
+  __device__ __forceinline__ void copy_table_set(int lg, int u) const {
 #pragma unroll
     for (int i = 0; i < kTableCopies; ++i) {
-      const int blk = pw * kTableCopies + i;
-      const unsigned off = blk * 1024 < tgb ? (unsigned)((size_t)g * tgb + blk * 1024 + lane * 16) : kOutOfRange;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rt, (__attribute__((address_space(3))) void*)(dst + blk * 1024), 16, off, 0, 0, 0);
+      const int slot = kTableCopies * pw + i;
+      const int fl = kCp == 8 ? 8 * (slot / 2) + 2 * u + slot % 2 : 8 * slot + u;
+      if (lane < 4 * L) {
+        const unsigned off = (unsigned)((size_t)(g0 + lg) * tgb + fl * 64 * L + lane * 16);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            rt, (__attribute__((address_space(3))) void*)(smem + kTblAt + ((u % 2) * kSetFeat + slot) * 64 * L), 16,
+            off, 0, 0, 0);
+      }
     }
   }
 
-  // The entries of spline chunk t's features (t + kCp * m, m < 32 / kCp) of group lg into
-  // the table buffer: producer wave pw < 32 / kCp copies feature t + kCp * pw, whose 64 L
-  // bytes are 4 L lanes of one direct-to-LDS instruction.
-  __device__ __forceinline__ void copy_table_slice(int lg, int t) const {
-    if (lane < 4 * L) {
-      const int fl = t + kCp * pw;
-      const unsigned off = (unsigned)((size_t)(g0 + lg) * tgb + fl * 64 * L + lane * 16);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rt, (__attribute__((address_space(3))) void*)(smem + kTblAt + fl * 64 * L), 16, off, 0, 0, 0);
-    }
-  }
-
-  // x at this lane's features xb .. xb + kX - 1 of group lg (past I or B: 0).
+  // x at this lane's features 8 fq .. 8 fq + 7 of group lg (past I or B: 0).
   __device__ __forceinline__ void load_x(int lg, float (&xs)[2][kX]) const {
     const int g = g0 + lg;
 #pragma unroll
@@ -610,7 +639,7 @@ struct Producer {
       if constexpr (kVec) {  // I % 4 == 0: a 4-feature run is wholly inside or past I
 #pragma unroll
         for (int v = 0; v < kX / 4; ++v) {
-          const int f = g * kGroup + xb + 4 * v;
+          const int f = g * kGroup + 8 * fq + 4 * v;
           const unsigned off = (row[rb] < B && f < I) ? (unsigned)(((size_t)row[rb] * I + f) * 4) : kOutOfRange;
           const f32x4 val = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0));
 #pragma unroll
@@ -619,7 +648,7 @@ struct Producer {
       } else {
 #pragma unroll
         for (int t = 0; t < kX; ++t) {
-          const int f = g * kGroup + xb + t;
+          const int f = g * kGroup + 8 * fq + t;
           const unsigned off = (row[rb] < B && f < I) ? (unsigned)(((size_t)row[rb] * I + f) * 4) : kOutOfRange;
           xs[rb][t] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rx, off, 0, 0));
         }
@@ -627,204 +656,239 @@ struct Producer {
     }
   }
 
-  // Chunk c's activations into stage c % 2: the lane's two row blocks evaluated, split and
-  // stored as their MFMA fragments.  A silu chunk (kT < 0) takes slots 8 fg .. 8 fg + 7 from
-  // the lane's x values 8 fg - xb ..; spline chunk kT expands feature xb + kT.
-  // The weight copies of chunk cw are issued in four pieces between the parts of the
-  // evaluation: a copy instruction holds the wave until the CU's memory pipeline takes it,
-  // so spreading them lets the evaluation's VALU work fill that time.
-  template <int kT>
-  __device__ __forceinline__ void prepare_act(int c, const float (&xs)[2][kX], int cw, f32x2& k01next) const {
-    uint8_t* act = smem + kActAt + (c & 1) * kActBytes;
-    copy_weights_piece<0>(cw);
-    // Both row blocks are evaluated before either is stored: a store to LDS orders every
-    // later LDS read after it, so interleaving would serialise the two lookups.
-    f16x8 hi[2], lo[2];
-    if constexpr (kT < 0) {
-#pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        float a[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          float xv = xs[rb][t];
-          if constexpr (kX > 8) {
-            // Both candidates as register values first: a select between two elements would
-            // otherwise become a runtime index, which keeps the array in scratch memory.
-            float xh = xs[rb][8 + t];
-            asm volatile("" : "+v"(xv), "+v"(xh));
-            xv = (fg & 1) ? xh : xv;
-          }
-          a[t] = silu(xv);
-        }
-        split8(a, hi[rb], lo[rb]);
-        if (rb == 0) copy_weights_piece<1>(cw);
-      }
-      copy_weights_piece<2>(cw);
+  // A feature's basis values at x (its table entry at `fe`).
+  __device__ __forceinline__ int feature_values(float x, const float* fe, float (&N)[4]) const {
+    TabFetch tf;
+    if (uniform) {
+      const f32x2 k01 = *reinterpret_cast<const f32x2*>(fe);
+      tf = tab_locate_uniform(x, k01.x, __builtin_amdgcn_rcpf(k01.y - k01.x), fe, L);
     } else {
-      const float* fe = reinterpret_cast<const float*>(smem + kTblAt + (xb + kT) * 64 * L);
-      TabFetch tf[2];
-      if (uniform) {
-        // The first two knots were read a step ago (k01); read the next spline chunk's now.
-        const f32x2 k01 = k01next;
-        k01next = *reinterpret_cast<const f32x2*>(smem + kTblAt + (xb + (kT + 1) % kX) * 64 * L);
-        const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
+      f32x4 kn[4];
+      tab_knots(fe, kn);
+      tf = tab_locate_count(x, kn, fe, L);
+    }
+    tab_values(x, tf, N);
+    return tf.j;
+  }
+
+  // Row block rb (of this wave's two) of step j's activations of a group into stage `st`:
+  // j = 0 the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline
+  // step u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).
+  template <int kJ>
+  __device__ __forceinline__ void prepare_rb(uint8_t* st, const float (&xs)[2][kX], int rb) const {
+    f16x8 hi, lo;
+    unsigned bits = 0;
+    float v[8];
+    if constexpr (kJ == 0) {
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_uniform(xs[rb][kT], k01.x, inv_h, fe, L);
+      for (int t = 0; t < 8; ++t) v[t] = silu(xs[rb][t]);
+    } else {
+      constexpr int u = kJ - 1;
+      const uint8_t* set = smem + kTblAt + (u % 2) * kSetFeat * 64 * L;
+      if constexpr (kCp == 8) {
+        float Na[4], Nb[4];
+        const int ja = feature_values(xs[rb][2 * u], reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), Na);
+        const int jb = feature_values(xs[rb][2 * u + 1], reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), Nb);
+        unsigned ba, bb;
+        sparse8(ja, Na, v, ba);
+        sparse8(jb, Nb, v + 4, bb);
+        bits = ba | (bb << 8);
       } else {
-        f32x4 kn[4];
-        tab_knots(fe, kn);
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb) tf[rb] = tab_locate_count(xs[rb][kT], kn, fe, L);
+        float N[4];
+        const int jj = feature_values(xs[rb][u], reinterpret_cast<const float*>(set + fq * 64 * L), N);
+        sparse16(jj, N, v, bits);
       }
-      copy_weights_piece<1>(cw);
-      tab_finish<kCp>(xs[0][kT], tf[0], (8 * fg) % kCp, hi[0], lo[0]);
-      copy_weights_piece<2>(cw);
-      tab_finish<kCp>(xs[1][kT], tf[1], (8 * fg) % kCp, hi[1], lo[1]);
     }
-    copy_weights_piece<3>(cw);
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int frag = 2 * pw + rb;
-      *reinterpret_cast<f16x8*>(act + ((frag * 2 + 0) * 64 + lane) * 16) = hi[rb];
-      *reinterpret_cast<f16x8*>(act + ((frag * 2 + 1) * 64 + lane) * 16) = lo[rb];
-    }
+    split8(v, hi, lo);
+    const int frag = 2 * pw + rb;
+    *reinterpret_cast<f16x8*>(st + ((frag * 2 + 0) * 64 + lane) * 16) = hi;
+    *reinterpret_cast<f16x8*>(st + ((frag * 2 + 1) * 64 + lane) * 16) = lo;
+    if constexpr (kJ > 0) *reinterpret_cast<unsigned*>(st + kActFragBytes + (frag * 64 + lane) * 4) = bits;
   }
 
-  // Step lg * kQ + kK runs while the consumers compute that chunk: it refills the entries
-  // of the spline chunk prepared in the previous step with the next group's, loads the next
-  // group's x at a group's first step, and writes the activations of chunk c = lg * kQ +
-  // kK + 1 (spline chunk kK of group lg, or for kK = kQ - 1 the next group's silu chunk).
-  // kLast: lg is the workgroup's last group.  Every condition is a constant, so
-  // the compiler's own waits for x stay exact (a merge of paths would make it wait for
-  // every load, the weight copies of the step included).
-  template <bool kLast, int kK>
-  __device__ __forceinline__ void step(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX], f32x2& k01) const {
-    const int c = lg * kQ + kK + 1;
-    constexpr bool kCopyNext = !kLast || kK + 2 < kQ;   // chunk c + 1 exists
-    constexpr bool kSlice = !kLast && kK >= 1;          // refill spline chunk kK - 1's entries
-    constexpr bool kXNext = !kLast && kK == 0;
-    // (only the waves with a feature of the slice issue its copy)
-    const bool slice = kSlice && pw < kGroup / kCp;
-    if (slice) copy_table_slice(lg + 1, kK - 1);
+  // Step s = lg * kQ + kJ (the consumers' phases of step s run meanwhile): see the
+  // schedule above.  kLast: lg is the workgroup's last group.  Every condition is a
+  // constant, so the waits count exactly the loads issued after the one awaited.
+  template <bool kLast, int kJ>
+  __device__ __forceinline__ void step(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX]) const {
+    const int s = lg * kQ + kJ;
+    constexpr bool kNext = !kLast || kJ + 1 < kQ;        // step s + 1 exists
+    constexpr int kNJ = (kJ + 1) % kQ;                   // its position in its group
+    constexpr int kPlane = kNJ == 0 ? kSubTileCopies : 2 * kSubTileCopies;
+    constexpr int kC = kNext ? kPlane : 0;               // copies of one of its planes
+    // The table set step s (spline step u = kJ - 1) used is refilled for spline step
+    // u + 2, of this group or the next.
+    constexpr int kU = kJ - 1, kU2 = kJ + 1;
+    constexpr bool kRefill = kJ >= 1 && (kU2 < kS || !kLast);
+    constexpr int kT = kRefill ? kTableCopies : 0;
+    constexpr bool kXNext = kJ == 0 && !kLast;
+    constexpr int kXn = kXNext ? kXLoads : 0;
+    const int lgn = kJ + 1 < kQ ? lg : lg + 1;
+    uint8_t* st = smem + kActAt + ((s + 1) & 1) * kActBytes;
+    (void)kU;
+
+    if constexpr (kRefill) {
+      if constexpr (kU2 < kS) copy_table_set(lg, kU2);
+      else copy_table_set(lg + 1, kU2 - kS);
+    }
     if constexpr (kXNext) load_x(lg + 1, xnext);
-    if constexpr (kK < kQ - 1) {
-      prepare_act<kK>(c, xcur, c + 1, k01);
-    } else if constexpr (!kLast) {
+    if constexpr (kNext) copy_step_plane<kNJ>(rlo, lgn, (2 * (s + 1)) % kSlots);
+    if constexpr (kNext) {
+      if constexpr (kNJ == 0) {
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb)
+        for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
-      prepare_act<-1>(c, xcur, c + 1, k01);
-    } else {
-      copy_weights_piece<0>(c + 1);  // past the last chunk: no copies
+          for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
+      }
+      prepare_rb<kNJ>(st, xcur, 0);
     }
-    // Everything issued before this step (chunk c's weights among it) has landed.
-    constexpr int kIssued = (kCopyNext ? kCopies : 0) + (kXNext ? kXLoads : 0);
-    if (slice) wait_vmcnt<kIssued + 1>();
-    else wait_vmcnt<kIssued>();
-    barrier_no_vm_drain();
+    wait_vmcnt<kT + kXn + kC>();  // hi(s) has landed
+    barrier_no_vm_drain();        // B(s)
+    if constexpr (kNext) copy_step_plane<kNJ>(rhi, lgn, (2 * (s + 1) + 1) % kSlots);
+    if constexpr (kNext) prepare_rb<kNJ>(st, xcur, 1);
+    wait_vmcnt<kC>();             // lo(s+1), the table set and x have landed
+    barrier_no_vm_drain();        // A(s+1)
   }
 
-  template <bool kLast, int... kKs>
-  __device__ __forceinline__ void group_steps(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX], f32x2& k01,
-                                              std::integer_sequence<int, kKs...>) const {
-    (step<kLast, kKs>(lg, xcur, xnext, k01), ...);
+  template <bool kLast, int... kJs>
+  __device__ __forceinline__ void group_steps(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX],
+                                              std::integer_sequence<int, kJs...>) const {
+    (step<kLast, kJs>(lg, xcur, xnext), ...);
   }
 
   __device__ void run() const {
     float xcur[2][kX], xnext[2][kX];
-    // Prologue: chunks 0 and 1's weights, the first group's table and x, chunk 0's
-    // activations; the barrier after it publishes them.
-    copy_weights(0);
-    if (nchunks > 1) copy_weights(1);
-    copy_table(0);
+    // Prologue: step 0's two planes, the table sets of the first group's spline steps 0 and
+    // 1, its x, and step 0's activations (silu); A(0) publishes them.
+    copy_step_plane<0>(rlo, 0, 0);
+    copy_step_plane<0>(rhi, 0, 1);
+    copy_table_set(0, 0);
+    if (kS > 1) copy_table_set(0, 1);
     load_x(0, xcur);
     wait_vmcnt<0>();
-    f32x2 k01;
-    prepare_act<-1>(0, xcur, nchunks, k01);  // (no copies: chunk 1's were issued above)
-    barrier_no_vm_drain();
-    // Spline chunk 0's first two knots: the whole table is visible after the barrier.
-    k01 = *reinterpret_cast<const f32x2*>(smem + kTblAt + xb * 64 * L);
-    // The steps of a group are unrolled, so every chunk kind is a constant.
-    for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, k01, std::make_integer_sequence<int, kQ>{});
-    group_steps<true>(nlg - 1, xcur, xnext, k01, std::make_integer_sequence<int, kQ>{});
+    uint8_t* st = smem + kActAt;
+    prepare_rb<0>(st, xcur, 0);
+    prepare_rb<0>(st, xcur, 1);
+    barrier_no_vm_drain();  // A(0)
+    for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, std::make_integer_sequence<int, kQ>{});
+    group_steps<true>(nlg - 1, xcur, xnext, std::make_integer_sequence<int, kQ>{});
   }
 };
 
-// Consumer: chunk c's 96 MFMAs, two row blocks at a time and term-major, so an
-// accumulator's next MFMA is 8 MFMAs behind its previous one (each accumulator sums
-// hi*hi, lo*hi, hi*lo per chunk, in that order).  The next pair's activation fragments are
-// read during a pair's MFMAs (one read per six MFMAs), so LDS reads overlap the MFMAs.
-__device__ __forceinline__ void consume_chunk(const uint8_t* wst, const uint8_t* ast, int wave, int lane,
-                                              f32x4 (&acc)[kRB][kCB]) {
-  const int fr = lane % 16, fg = lane / 16;
-  f16x8 wh[kCB], wl[kCB];
+// Consumer phases.  A step's weight fragments: lane (column fr of block cb, quarter fq)
+// reads k = 8 fq .. 8 fq + 7 of each sub-tile (the sparse B operand takes both, k and
+// k + 32 of the step).  Activation fragments of two row blocks are read during the previous
+// pair's MFMAs.
+__device__ __forceinline__ f16x8 wfrag(const uint8_t* sub, int wave, int cb, int lane) {
+  const int r = wave * (kCB * 16) + cb * 16 + lane % 16;
+  return __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(sub + swizzle64(r, lane / 16)));
+}
+
+typedef _Float16 f16x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f16x16 join16(f16x8 a, f16x8 b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
+struct ActPair {
+  f16x8 h[2], l[2];
+  int idx[2];
+};
+
+template <bool kLo>
+__device__ __forceinline__ void read_act(const uint8_t* ast, int lane, int rb, ActPair& a) {
 #pragma unroll
-  for (int cb = 0; cb < kCB; ++cb) {
-    const int r = wave * (kCB * 16) + cb * 16 + fr;
-    wh[cb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(wst + swizzle64(r, fg)));
-    wl[cb] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(wst + kWHalfBytes + swizzle64(r, fg)));
-  }
-  const uint8_t* act = ast + lane * 16;
-  auto read_pair = [&](int rb, f16x8 (&ah)[2], f16x8 (&al)[2]) {
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      ah[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(act + ((rb + r) * 2 + 0) * 1024));
-      al[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(act + ((rb + r) * 2 + 1) * 1024));
-    }
-  };
-  f16x8 ah[2], al[2];
-  read_pair(0, ah, al);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int rb = 0; rb < kRB; rb += 2) {
-    f16x8 nh[2], nl[2];
-    if (rb + 2 < kRB) read_pair(rb + 2, nh, nl);
-#pragma unroll
-    for (int term = 0; term < 3; ++term)
-#pragma unroll
-      for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int cb = 0; cb < kCB; ++cb)
-          acc[rb + r][cb] = mfma16(term == 1 ? wl[cb] : wh[cb], term == 2 ? al[r] : ah[r], acc[rb + r][cb]);
-    if (rb + 2 < kRB) {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);  // 6 MFMAs
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if (rb + 2 < kRB) {
-#pragma unroll
-      for (int r = 0; r < 2; ++r) {
-        ah[r] = nh[r];
-        al[r] = nl[r];
-      }
-    }
+  for (int r = 0; r < 2; ++r) {
+    a.h[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(ast + (((rb + r) * 2 + 0) * 64 + lane) * 16));
+    if constexpr (kLo)
+      a.l[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(ast + (((rb + r) * 2 + 1) * 64 + lane) * 16));
+    a.idx[r] = *reinterpret_cast<const int*>(ast + kActFragBytes + ((rb + r) * 64 + lane) * 4);
   }
 }
 
-// Output slot of a consumer accumulator: consumer wave wq, row block rb, column block cb,
-// lane lq hold columns n0 + 64 wq + 16 cb + 4 (lq / 16) + 0..3 of batch row m0 + 16 rb +
-// lq % 16, scaled back by the columns' scales.
-__device__ __forceinline__ void store_slot(f32x4 val, int wq, int rb, int cb, int lq, int m0, int n0, int B, int O,
-                                           const float* __restrict__ colscale, __amdgpu_buffer_rsrc_t ro, bool vec) {
-  const int o = n0 + wq * (kCB * 16) + cb * 16 + 4 * (lq / 16);
-  const int row = m0 + rb * 16 + lq % 16;
-  val *= *reinterpret_cast<const f32x4*>(colscale + o);
-  if (vec) {
-    const unsigned off = (row < B && o < O) ? (unsigned)(((size_t)row * O + o) * 4) : kOutOfRange;
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, val), ro, off, 0, 0);
-  } else {
+// Phase L (kH false: hi_a * lo_w) or H (hi_a * hi_w, then lo_a * hi_w) of one step, from the
+// weight plane in `slot` and the activations in `ast`.
+template <bool kSparse, bool kH>
+__device__ __forceinline__ void consume_phase(const uint8_t* slot, const uint8_t* ast, int wave, int lane,
+                                              f32x4 (&acc)[kRB][kCB]) {
+  f16x8 w0[kCB], w1[kCB];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const unsigned off = (row < B && o + e < O) ? (unsigned)(((size_t)row * O + o + e) * 4) : kOutOfRange;
-      // Through a scalar: hipcc turned __builtin_bit_cast(unsigned, val[e]) into a store of
-      // element 0 for every e.
-      const float ve = val[e];
-      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ve), ro, off, 0, 0);
+  for (int cb = 0; cb < kCB; ++cb) {
+    w0[cb] = wfrag(slot, wave, cb, lane);
+    if constexpr (kSparse) w1[cb] = wfrag(slot + kSubTileBytes, wave, cb, lane);
+  }
+  ActPair cur;
+  read_act<kH>(ast, lane, 0, cur);
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int kTerms = kH ? 2 : 1;
+  constexpr int kReads = kH ? 6 : 4;  // LDS reads of a pair
+#pragma unroll
+  for (int rb = 0; rb < kRB; rb += 2) {
+    ActPair nxt;
+    if (rb + 2 < kRB) read_act<kH>(ast, lane, rb + 2, nxt);
+#pragma unroll
+    for (int term = 0; term < kTerms; ++term)
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int cb = 0; cb < kCB; ++cb) {
+          const f16x8 a = term == 0 ? cur.h[r] : cur.l[r];
+          if constexpr (kSparse)
+            acc[rb + r][cb] = __builtin_amdgcn_smfmac_f32_16x16x64_f16(a, join16(w0[cb], w1[cb]), acc[rb + r][cb],
+                                                                       cur.idx[r], 0, 0);
+          else
+            acc[rb + r][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, w0[cb], acc[rb + r][cb], 0, 0, 0);
+        }
+    if (rb + 2 < kRB) {
+#pragma unroll
+      for (int u = 0; u < kReads; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
+        __builtin_amdgcn_sched_group_barrier(0x008, 8 * kTerms / kReads, 0);      // MFMAs
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (rb + 2 < kRB) cur = nxt;
+  }
+}
+
+template <int kCp>
+struct Consumer {
+  static constexpr int kS = kCp / 2;
+  static constexpr int kQ = 1 + kS;
+
+  template <int kJ>
+  __device__ __forceinline__ void step(int s, int wave, int lane, f32x4 (&acc)[kRB][kCB]) const {
+    const uint8_t* ast = smem + kActAt + (s & 1) * kActBytes;
+    consume_phase<(kJ > 0), false>(smem + ((2 * s) % kSlots) * kSlotBytes, ast, wave, lane, acc);
+    barrier_no_vm_drain();  // B(s)
+    consume_phase<(kJ > 0), true>(smem + ((2 * s + 1) % kSlots) * kSlotBytes, ast, wave, lane, acc);
+    barrier_no_vm_drain();  // A(s+1)
+  }
+
+  template <int... kJs>
+  __device__ __forceinline__ void group(int lg, int wave, int lane, f32x4 (&acc)[kRB][kCB],
+                                        std::integer_sequence<int, kJs...>) const {
+    (step<kJs>(lg * kQ + kJs, wave, lane, acc), ...);
+  }
+
+  uint8_t* smem;
+};
+
+// Output of a consumer accumulator: consumer wave wq, row block rb, column block cb, lane
+// lq hold output column n0 + 64 wq + 16 cb + lq % 16 of batch rows m0 + 16 rb + 4 (lq / 16)
+// + 0..3, scaled back by the column's scale.
+__device__ __forceinline__ void store_slot(f32x4 val, int wq, int rb, int cb, int lq, int m0, int n0, int B, int O,
+                                           const float* __restrict__ colscale, __amdgpu_buffer_rsrc_t ro) {
+  const int o = n0 + wq * (kCB * 16) + cb * 16 + lq % 16;
+  const float sc = colscale[o];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int row = m0 + rb * 16 + 4 * (lq / 16) + e;
+    const unsigned off = (row < B && o < O) ? (unsigned)(((size_t)row * O + o) * 4) : kOutOfRange;
+    // Through a scalar: hipcc turned __builtin_bit_cast(unsigned, val[e]) into a store of
+    // element 0 for every e.
+    const float ve = val[e] * sc;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(ve), ro, off, 0, 0);
   }
 }
 
@@ -833,7 +897,6 @@ __device__ __forceinline__ void store_slot(f32x4 val, int wq, int rb, int cb, in
 // sums the nsplit partials of every slot in split order (so the result does not depend on
 // which split arrives last), 16 slots per thread with each split's loads in flight
 // together, resets the counter and writes the output.
-template <bool kVec>
 __device__ __forceinline__ void split_k_finish(uint8_t* smem, int tid, int split, int nsplit, int tile, int m0,
                                                int n0, int B, int O, const float* __restrict__ colscale,
                                                float* __restrict__ out, const float* __restrict__ partial,
@@ -850,8 +913,8 @@ __device__ __forceinline__ void split_k_finish(uint8_t* smem, int tid, int split
   __syncthreads();
   if (!*flag) return;
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  constexpr int kSlots = BM * BN / 4;           // 16-byte slots per tile
-  constexpr int kPer = kSlots / kThreads;       // per thread
+  constexpr int kTileSlots = BM * BN / 4;        // 16-byte slots per tile
+  constexpr int kPer = kTileSlots / kThreads;    // per thread
   const int tiles = gridDim.x / nsplit;
   const size_t split_stride = (size_t)tiles * (BM * BN);
   const float* first = partial + (size_t)tile * (BM * BN);
@@ -869,13 +932,10 @@ __device__ __forceinline__ void split_k_finish(uint8_t* smem, int tid, int split
   for (int u = 0; u < kPer; ++u) {
     const int sl = tid + u * kThreads;  // = ((wq * kRB + rb) * kCB + cb) * 64 + lq
     const int lq = sl % kWave, cb = (sl / kWave) % kCB, rb = (sl / (kWave * kCB)) % kRB, wq = sl / (kWave * kCB * kRB);
-    store_slot(sum[u], wq, rb, cb, lq, m0, n0, B, O, colscale, ro, kVec);
+    store_slot(sum[u], wq, rb, cb, lq, m0, n0, B, O, colscale, ro);
   }
 }
 
-// kVec: I and O multiples of 4, x and out 16-byte aligned (16-byte loads and stores);
-// otherwise 4-byte ones.
-//
 // Split-K (nsplit > 1, for grids of fewer tiles than CUs): workgroup b computes split
 // b % nsplit, feature groups [split*gper, split*gper + gper), of tile b / nsplit.  It
 // writes its fp32 partial tile to `partial` and arrives on the tile's counter; the last
@@ -888,11 +948,11 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
     const _Float16* __restrict__ blo, const float* __restrict__ colscale, float* __restrict__ out, int nsplit,
     int gper, float* __restrict__ partial, unsigned* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr int kQ = 1 + kCp;
+  constexpr int kQ = 1 + kCp / 2;
   const int tm = (B + BM - 1) / BM, tn = Opad / BN;
   const int split = blockIdx.x % nsplit, tile = blockIdx.x / nsplit;
   const int g0 = split * gper, g1 = min(ngroups, g0 + gper);
-  const int nchunks = (g1 - g0) * kQ;
+  const int nlg = g1 - g0;
   int mt, nt;
   tile_of(tile, tm, tn, mt, nt);
   const int m0 = mt * BM, n0 = nt * BN;
@@ -904,13 +964,12 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
       Producer<kCp, kVec> p;
       p.smem = smem;
       p.I = I; p.L = L; p.B = B; p.Opad = Opad; p.n0 = n0;
-      p.g0 = g0; p.nlg = g1 - g0; p.nchunks = nchunks;
-      p.lane = lane; p.fr = lane % 16; p.fg = lane / 16; p.pw = wave - kConsumerWaves;
-      p.xb = ((8 * p.fg) / kCp) * kCp;
+      p.g0 = g0; p.nlg = nlg;
+      p.lane = lane; p.fr = lane % 16; p.fq = lane / 16; p.pw = wave - kConsumerWaves;
       p.row[0] = m0 + 32 * p.pw + p.fr;
       p.row[1] = p.row[0] + 16;
       p.tgb = tbl_group_bytes(L);
-      const size_t wbytes = (size_t)ngroups * kQ * Opad * kChunk * 2;
+      const size_t wbytes = (size_t)ngroups * (1 + kCp) * Opad * kChunk * 2;
       p.rhi = make_rsrc(bhi, wbytes);
       p.rlo = make_rsrc(blo, wbytes);
       p.rx = make_rsrc(x, (size_t)B * I * 4);
@@ -921,7 +980,7 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
       p.run();
     }
     wait_vmcnt<0>();  // no copy may still be writing LDS past this point
-    if (nsplit > 1) split_k_finish<kVec>(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
+    if (nsplit > 1) split_k_finish(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
     return;
   }
 
@@ -930,11 +989,10 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
   for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  barrier_no_vm_drain();  // stage 0 is ready
-  for (int c = 0; c < nchunks; ++c) {
-    consume_chunk(smem + (c % kWStages) * kWStageBytes, smem + kActAt + (c & 1) * kActBytes, wave, lane, acc);
-    barrier_no_vm_drain();
-  }
+  barrier_no_vm_drain();  // A(0)
+  Consumer<kCp> cons;
+  cons.smem = smem;
+  for (int lg = 0; lg < nlg; ++lg) cons.group(lg, wave, lane, acc, std::make_integer_sequence<int, kQ>{});
 
   if (nsplit > 1) {
     // This thread's 16-byte slots of the partial tile: (wave, rb, cb, lane), so every
@@ -946,7 +1004,7 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
 #pragma unroll
       for (int cb = 0; cb < kCB; ++cb)
         *reinterpret_cast<f32x4*>(mine + (((wave * kRB + rb) * kCB + cb) * kWave + lane) * 4) = acc[rb][cb];
-    split_k_finish<kVec>(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
+    split_k_finish(smem, tid, split, nsplit, tile, m0, n0, B, O, colscale, out, partial, counters);
     return;
   }
 
@@ -955,7 +1013,7 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
 #pragma unroll
   for (int cb = 0; cb < kCB; ++cb)
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) store_slot(acc[rb][cb], wave, rb, cb, lane, m0, n0, B, O, colscale, ro, kVec);
+    for (int rb = 0; rb < kRB; ++rb) store_slot(acc[rb][cb], wave, rb, cb, lane, m0, n0, B, O, colscale, ro);
 }
 
 }  // namespace kan
