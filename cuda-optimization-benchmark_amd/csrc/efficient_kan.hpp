@@ -572,15 +572,15 @@ __device__ __forceinline__ void sparse16(int j, const float (&N)[4], float* v, u
 // 4 part + 3 of each sub-tile.  A direct-to-LDS instruction writes 64 consecutive 16-byte
 // slots (16 rows of 64 bytes); lane i fetches the chunk the swizzle places in slot i.
 constexpr int kSubTileCopies = BN / 16 / 4;  // 1 KiB copies per copying wave per sub-tile
-template <int kSub>
+template <int kSub, int kPiece = 0, int kPieces = 1>
 __device__ __forceinline__ void copy_half_tile(uint8_t* smem, __amdgpu_buffer_rsrc_t rp, int slot, int q, int Opad,
                                                int n0, int part, int lane) {
   uint8_t* st = smem + slot * kSlotBytes;
   const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
+  constexpr int kAll = kSub * kSubTileCopies, kPer = kAll / kPieces;
 #pragma unroll
-  for (int t = 0; t < kSub; ++t)
-#pragma unroll
-    for (int i = 0; i < kSubTileCopies; ++i) {
+  for (int n = kPiece * kPer; n < (kPiece + 1) * kPer; ++n) {
+      const int t = n / kSubTileCopies, i = n % kSubTileCopies;
       const int group = part * kSubTileCopies + i;
       const unsigned off = (unsigned)(((size_t)(q + t) * Opad + n0 + group * 16 + r16) * 64 + 16 * logical);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -608,10 +608,11 @@ struct Producer {
   int tgb;
 
   // Half-tiles of step s = lg * kQ + j (j = 0: silu, one sub-tile).
-  template <int kJ>
+  template <int kJ, int kPiece = 0, int kPieces = 1>
   __device__ __forceinline__ void copy_step_plane(__amdgpu_buffer_rsrc_t rp, int lg, int slot) const {
     const int q = (g0 + lg) * kChunksPerGroup + (kJ == 0 ? 0 : 2 * kJ - 1);
-    copy_half_tile<kJ == 0 ? 1 : 2>(smem, rp, slot, q, Opad, n0, pw, lane);
+    copy_half_tile<kJ == 0 ? 1 : 2, kPiece, kPieces>(smem, rp, slot, q, Opad, n0, pw, lane);
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   // The table entries of spline step u's features of group lg into set u % 2: this wave
@@ -656,54 +657,92 @@ struct Producer {
     }
   }
 
-  // A feature's basis values at x (its table entry at `fe`).
-  __device__ __forceinline__ int feature_values(float x, const float* fe, float (&N)[4]) const {
-    TabFetch tf;
+  // Both row blocks' basis values of one feature (its table entry at `fe`): the knots are
+  // read once for the two, and the two lookups' table reads go out together.
+  __device__ __forceinline__ void feature_values(const float* fe, float x0, float x1, float (&N0)[4], float (&N1)[4],
+                                                 int& j0, int& j1) const {
+    TabFetch t0, t1;
     if (uniform) {
       const f32x2 k01 = *reinterpret_cast<const f32x2*>(fe);
-      tf = tab_locate_uniform(x, k01.x, __builtin_amdgcn_rcpf(k01.y - k01.x), fe, L);
+      const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
+      t0 = tab_locate_uniform(x0, k01.x, inv_h, fe, L);
+      t1 = tab_locate_uniform(x1, k01.x, inv_h, fe, L);
     } else {
       f32x4 kn[4];
       tab_knots(fe, kn);
-      tf = tab_locate_count(x, kn, fe, L);
+      t0 = tab_locate_count(x0, kn, fe, L);
+      t1 = tab_locate_count(x1, kn, fe, L);
     }
-    tab_values(x, tf, N);
-    return tf.j;
+    tab_values(x0, t0, N0);
+    tab_values(x1, t1, N1);
+    j0 = t0.j;
+    j1 = t1.j;
   }
 
-  // Row block rb (of this wave's two) of step j's activations of a group into stage `st`:
-  // j = 0 the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline
-  // step u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).
-  template <int kJ>
-  __device__ __forceinline__ void prepare_rb(uint8_t* st, const float (&xs)[2][kX], int rb) const {
-    f16x8 hi, lo;
-    unsigned bits = 0;
-    float v[8];
+  // Step j's activations of a group, both of this wave's row blocks, into stage `st`: j = 0
+  // the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline step
+  // u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).  The
+  // four pieces of step jc's plane of group lgc go out between the parts: a copy instruction
+  // holds the wave until the CU's memory pipeline takes it, so spreading them lets the
+  // evaluation's VALU work fill that time.
+  template <int kJ, int kJc, bool kCopy>
+  __device__ __forceinline__ void prepare(uint8_t* st, const float (&xs)[2][kX], __amdgpu_buffer_rsrc_t rp, int lgc,
+                                          int slot) const {
+    auto piece = [&](auto k) {
+      if constexpr (kCopy) copy_step_plane<kJc, decltype(k)::value, 4>(rp, lgc, slot);
+    };
+    float v[2][8];
+    unsigned bits[2] = {0u, 0u};
+    piece(std::integral_constant<int, 0>{});
     if constexpr (kJ == 0) {
 #pragma unroll
-      for (int t = 0; t < 8; ++t) v[t] = silu(xs[rb][t]);
+      for (int rb = 0; rb < 2; ++rb) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) v[rb][t] = silu(xs[rb][t]);
+        if (rb == 0) piece(std::integral_constant<int, 1>{});
+      }
+      piece(std::integral_constant<int, 2>{});
     } else {
       constexpr int u = kJ - 1;
       const uint8_t* set = smem + kTblAt + (u % 2) * kSetFeat * 64 * L;
       if constexpr (kCp == 8) {
-        float Na[4], Nb[4];
-        const int ja = feature_values(xs[rb][2 * u], reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), Na);
-        const int jb = feature_values(xs[rb][2 * u + 1], reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), Nb);
-        unsigned ba, bb;
-        sparse8(ja, Na, v, ba);
-        sparse8(jb, Nb, v + 4, bb);
-        bits = ba | (bb << 8);
+        float Na[2][4], Nb[2][4];
+        int ja[2], jb[2];
+        feature_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
+                       Na[1], ja[0], ja[1]);
+        piece(std::integral_constant<int, 1>{});
+        feature_values(reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), xs[0][2 * u + 1],
+                       xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1]);
+        piece(std::integral_constant<int, 2>{});
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) {
+          unsigned ba, bb;
+          sparse8(ja[rb], Na[rb], v[rb], ba);
+          sparse8(jb[rb], Nb[rb], v[rb] + 4, bb);
+          bits[rb] = ba | (bb << 8);
+        }
       } else {
-        float N[4];
-        const int jj = feature_values(xs[rb][u], reinterpret_cast<const float*>(set + fq * 64 * L), N);
-        sparse16(jj, N, v, bits);
+        float N[2][4];
+        int jj[2];
+        feature_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
+                       jj[1]);
+        piece(std::integral_constant<int, 1>{});
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb) sparse16(jj[rb], N[rb], v[rb], bits[rb]);
+        piece(std::integral_constant<int, 2>{});
       }
     }
-    split8(v, hi, lo);
-    const int frag = 2 * pw + rb;
-    *reinterpret_cast<f16x8*>(st + ((frag * 2 + 0) * 64 + lane) * 16) = hi;
-    *reinterpret_cast<f16x8*>(st + ((frag * 2 + 1) * 64 + lane) * 16) = lo;
-    if constexpr (kJ > 0) *reinterpret_cast<unsigned*>(st + kActFragBytes + (frag * 64 + lane) * 4) = bits;
+    f16x8 hi[2], lo[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) split8(v[rb], hi[rb], lo[rb]);
+    piece(std::integral_constant<int, 3>{});
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int frag = 2 * pw + rb;
+      *reinterpret_cast<f16x8*>(st + ((frag * 2 + 0) * 64 + lane) * 16) = hi[rb];
+      *reinterpret_cast<f16x8*>(st + ((frag * 2 + 1) * 64 + lane) * 16) = lo[rb];
+      if constexpr (kJ > 0) *reinterpret_cast<unsigned*>(st + kActFragBytes + (frag * 64 + lane) * 4) = bits[rb];
+    }
   }
 
   // Step s = lg * kQ + kJ (the consumers' phases of step s run meanwhile): see the
@@ -716,23 +755,21 @@ struct Producer {
     constexpr int kNJ = (kJ + 1) % kQ;                   // its position in its group
     constexpr int kPlane = kNJ == 0 ? kSubTileCopies : 2 * kSubTileCopies;
     constexpr int kC = kNext ? kPlane : 0;               // copies of one of its planes
-    // The table set step s (spline step u = kJ - 1) used is refilled for spline step
-    // u + 2, of this group or the next.
-    constexpr int kU = kJ - 1, kU2 = kJ + 1;
+    // The table set step s (spline step kJ - 1) used is refilled for spline step kJ + 1,
+    // of this group or the next.
+    constexpr int kU2 = kJ + 1;
     constexpr bool kRefill = kJ >= 1 && (kU2 < kS || !kLast);
     constexpr int kT = kRefill ? kTableCopies : 0;
     constexpr bool kXNext = kJ == 0 && !kLast;
     constexpr int kXn = kXNext ? kXLoads : 0;
     const int lgn = kJ + 1 < kQ ? lg : lg + 1;
     uint8_t* st = smem + kActAt + ((s + 1) & 1) * kActBytes;
-    (void)kU;
 
     if constexpr (kRefill) {
       if constexpr (kU2 < kS) copy_table_set(lg, kU2);
       else copy_table_set(lg + 1, kU2 - kS);
     }
     if constexpr (kXNext) load_x(lg + 1, xnext);
-    if constexpr (kNext) copy_step_plane<kNJ>(rlo, lgn, (2 * (s + 1)) % kSlots);
     if constexpr (kNext) {
       if constexpr (kNJ == 0) {
 #pragma unroll
@@ -740,13 +777,13 @@ struct Producer {
 #pragma unroll
           for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
       }
-      prepare_rb<kNJ>(st, xcur, 0);
+      // hi(s+1), in pieces between the parts of step s+1's activations
+      prepare<kNJ, kNJ, true>(st, xcur, rhi, lgn, (2 * (s + 1)) % kSlots);
     }
-    wait_vmcnt<kT + kXn + kC>();  // hi(s) has landed
+    wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
     barrier_no_vm_drain();        // B(s)
-    if constexpr (kNext) copy_step_plane<kNJ>(rhi, lgn, (2 * (s + 1) + 1) % kSlots);
-    if constexpr (kNext) prepare_rb<kNJ>(st, xcur, 1);
-    wait_vmcnt<kC>();             // lo(s+1), the table set and x have landed
+    if constexpr (kNext) copy_step_plane<kNJ>(rlo, lgn, (2 * (s + 1) + 1) % kSlots);
+    wait_vmcnt<kC>();             // hi(s+1), the table set and x have landed
     barrier_no_vm_drain();        // A(s+1)
   }
 
@@ -760,15 +797,13 @@ struct Producer {
     float xcur[2][kX], xnext[2][kX];
     // Prologue: step 0's two planes, the table sets of the first group's spline steps 0 and
     // 1, its x, and step 0's activations (silu); A(0) publishes them.
-    copy_step_plane<0>(rlo, 0, 0);
-    copy_step_plane<0>(rhi, 0, 1);
+    copy_step_plane<0>(rhi, 0, 0);
+    copy_step_plane<0>(rlo, 0, 1);
     copy_table_set(0, 0);
     if (kS > 1) copy_table_set(0, 1);
     load_x(0, xcur);
     wait_vmcnt<0>();
-    uint8_t* st = smem + kActAt;
-    prepare_rb<0>(st, xcur, 0);
-    prepare_rb<0>(st, xcur, 1);
+    prepare<0, 0, false>(smem + kActAt, xcur, rhi, 0, 0);
     barrier_no_vm_drain();  // A(0)
     for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, std::make_integer_sequence<int, kQ>{});
     group_steps<true>(nlg - 1, xcur, xnext, std::make_integer_sequence<int, kQ>{});
@@ -859,9 +894,9 @@ struct Consumer {
   template <int kJ>
   __device__ __forceinline__ void step(int s, int wave, int lane, f32x4 (&acc)[kRB][kCB]) const {
     const uint8_t* ast = smem + kActAt + (s & 1) * kActBytes;
-    consume_phase<(kJ > 0), false>(smem + ((2 * s) % kSlots) * kSlotBytes, ast, wave, lane, acc);
+    consume_phase<(kJ > 0), true>(smem + ((2 * s) % kSlots) * kSlotBytes, ast, wave, lane, acc);
     barrier_no_vm_drain();  // B(s)
-    consume_phase<(kJ > 0), true>(smem + ((2 * s + 1) % kSlots) * kSlotBytes, ast, wave, lane, acc);
+    consume_phase<(kJ > 0), false>(smem + ((2 * s + 1) % kSlots) * kSlotBytes, ast, wave, lane, acc);
     barrier_no_vm_drain();  // A(s+1)
   }
 
