@@ -134,17 +134,21 @@ __host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, in
     for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
 }
 
-// Whether a knot row is uniform enough for the GEMM's direct interval lookup: h > 0 and
-// every knot within 1e-3 h of t_0 + k h (the grids efficient-kan builds, arange * h + a
-// in fp32, are uniform to a few ulps).
-__host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, int L) {
+// Whether a knot row is uniform to within rel: h > 0 and every knot within rel * h of
+// t_0 + k h.  Within 1e-3 h the GEMM's direct interval lookup is exact enough; within 1e-5 h
+// the bases are the cardinal cubic pieces to ~1e-5 of a basis value, so the GEMM may
+// evaluate those instead of the table's per-interval cubics (the grids efficient-kan builds,
+// arange * h + a in fp32, are uniform to a few ulps: ~1e-6 h).
+__host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, int L, double rel) {
   if (L < 2) return false;
   const double h = ((double)t[L - 1] - (double)t[0]) / (L - 1);
   if (!(h > 0.0) || !(h < 1e300)) return false;
   for (int k = 0; k < L; ++k)
-    if (!(__builtin_fabs((double)t[k] - ((double)t[0] + k * h)) <= 1e-3 * h)) return false;
+    if (!(__builtin_fabs((double)t[k] - ((double)t[0] + k * h)) <= rel * h)) return false;
   return true;
 }
+constexpr double kUniformRel = 1e-3;   // direct interval lookup
+constexpr double kCardinalRel = 1e-5;  // cardinal pieces in place of the table's cubics
 
 // ---------------------------------------------------------------------------------------
 // Weight preparation, one launch (kan_pack): each output column's scale, the GEMM's A
@@ -182,21 +186,24 @@ __host__ __device__ constexpr int spline_basis(int s) {
 }
 
 // Basis tables, one thread per table entry (L per feature: the knot row and the L - 1
-// intervals), kThreadsPerBlock entries per workgroup; uflags[block] = 1 when every knot
-// row the block wrote is uniform (kan_knots_uniform), else 0.
+// intervals), kThreadsPerBlock entries per workgroup; uflags[block] bit 0: every knot row
+// the block wrote is uniform to 1e-3 h, bit 1: to 1e-5 h (kan_knots_uniform).
 template <int kThreadsPerBlock>
 __device__ __forceinline__ void kan_tables_block(int block, const float* __restrict__ grid, int I, int L,
                                                  int ngroups, float* __restrict__ tables,
                                                  int* __restrict__ uflags) {
   const int idx = block * kThreadsPerBlock + (int)threadIdx.x;
   const int f = idx / L, j = idx % L - 1;
-  bool uniform = true;
+  bool uniform = true, cardinal = true;
   if (f < ngroups * kGroup) {
     float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
                                           (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
     if (f < I) {
       kan_table_entry(grid + (size_t)f * L, L, j, dst);
-      if (j < 0) uniform = kan_knots_uniform(grid + (size_t)f * L, L);
+      if (j < 0) {
+        uniform = kan_knots_uniform(grid + (size_t)f * L, L, kUniformRel);
+        cardinal = kan_knots_uniform(grid + (size_t)f * L, L, kCardinalRel);
+      }
     } else if (j < 0) {  // missing feature: knots 0, 1, 2, ... and zero coefficients
       for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
     } else {
@@ -204,7 +211,8 @@ __device__ __forceinline__ void kan_tables_block(int block, const float* __restr
     }
   }
   uniform = __syncthreads_and(uniform);
-  if (threadIdx.x == 0) uflags[block] = uniform ? 1 : 0;
+  cardinal = __syncthreads_and(cardinal);
+  if (threadIdx.x == 0) uflags[block] = (uniform ? 1 : 0) | (cardinal ? 2 : 0);
 }
 
 // kan_pack: the first tblocks workgroups build the basis tables (kan_tables_block); they
@@ -535,6 +543,43 @@ __device__ __forceinline__ void sparse16(int j, const float (&N)[4], float* v, u
   }
 }
 
+// The four bases j-3 .. j nonzero on interval j of a uniform knot row, at t = (x - t_j) / h in
+// [0, 1): the cardinal cubic B-spline pieces (1-t)^3/6, t^3/2 - t^2 + 2/3,
+// -t^3/2 + t^2/2 + t/2 + 1/6 and t^3/6.  Bases outside [0, C) and x outside the knot span
+// give zero.
+__device__ __forceinline__ void cardinal_pieces(float t, int j, int C, bool inside, float (&P)[4]) {
+  const float t2 = t * t, t3 = t2 * t, s = 1.0f - t;
+  P[0] = s * s * s * (1.0f / 6.0f);
+  P[1] = fmaf(0.5f, t3, 2.0f / 3.0f - t2);
+  P[2] = fmaf(-0.5f, t3, fmaf(0.5f, t2 + t, 1.0f / 6.0f));
+  P[3] = t3 * (1.0f / 6.0f);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int b = j - 3 + i;
+    P[i] = (inside && b >= 0 && b < C) ? P[i] : 0.0f;
+  }
+}
+
+// sparse8 from the bases in window order (P[i] is basis j - 3 + i).
+__device__ __forceinline__ void sparse8w(int j, const float (&P)[4], float* v, unsigned& bits) {
+  const bool jo = (j & 1) != 0;  // the first even basis is j - 3 (j odd) or j - 2
+  unsigned pe, po;
+  sparse_pair(jo ? (j - 3) >> 1 : (j - 2) >> 1, jo ? P[0] : P[1], jo ? P[2] : P[3], v[0], v[1], pe);
+  sparse_pair(jo ? (j - 3) >> 1 : (j - 4) >> 1, jo ? P[1] : P[0], jo ? P[3] : P[2], v[2], v[3], po);
+  bits = pe | (po << 4);
+}
+
+// sparse16 from the bases in window order.
+__device__ __forceinline__ void sparse16w(int j, const float (&P)[4], float* v, unsigned& bits) {
+  float N[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int i = (r - (j - 3)) & 3;  // window index of the basis = r (mod 4)
+    N[r] = i == 0 ? P[0] : (i == 1 ? P[1] : (i == 2 ? P[2] : P[3]));
+  }
+  sparse16(j, N, v, bits);
+}
+
 // kVec: O and I multiples of 4 and out, x 16-byte aligned (16-byte x loads); otherwise
 // 4-byte ones.  kUniform: every knot row passed kan_knots_uniform.
 
@@ -605,6 +650,8 @@ struct Producer {
   int lane, fr, fq, pw;
   int row[2];      // this lane's batch rows (global) for its two row blocks
   bool uniform;    // every knot row is uniform: direct interval lookup
+  bool cardinal;   // every knot row is uniform to 1e-5 h: cardinal pieces, no table cubics
+  int C;           // bases per feature
   int tgb;
 
   // Half-tiles of step s = lg * kQ + j (j = 0: silu, one sub-tile).
@@ -679,6 +726,20 @@ struct Producer {
     j1 = t1.j;
   }
 
+  // Both row blocks' bases of one feature on a cardinal knot row, in window order: the
+  // knots t_0, t_1 read once for the two, then each row's interval knot t_j.
+  __device__ __forceinline__ void cardinal_values(const float* fe, float x0, float x1, float (&P0)[4], float (&P1)[4],
+                                                  int& j0, int& j1) const {
+    const f32x2 k01 = *reinterpret_cast<const f32x2*>(fe);
+    const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
+    const int r0 = (int)__builtin_floorf((x0 - k01.x) * inv_h), r1 = (int)__builtin_floorf((x1 - k01.x) * inv_h);
+    j0 = min(max(r0, 0), L - 2);
+    j1 = min(max(r1, 0), L - 2);
+    const float tj0 = fe[j0], tj1 = fe[j1];
+    cardinal_pieces((x0 - tj0) * inv_h, j0, C, r0 == j0, P0);
+    cardinal_pieces((x1 - tj1) * inv_h, j1, C, r1 == j1, P1);
+  }
+
   // Step j's activations of a group, both of this wave's row blocks, into stage `st`: j = 0
   // the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline step
   // u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).  The
@@ -708,6 +769,21 @@ struct Producer {
       if constexpr (kCp == 8) {
         float Na[2][4], Nb[2][4];
         int ja[2], jb[2];
+        if (cardinal) {
+          cardinal_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
+                          Na[1], ja[0], ja[1]);
+          piece(std::integral_constant<int, 1>{});
+          cardinal_values(reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), xs[0][2 * u + 1],
+                          xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1]);
+          piece(std::integral_constant<int, 2>{});
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) {
+            unsigned ba, bb;
+            sparse8w(ja[rb], Na[rb], v[rb], ba);
+            sparse8w(jb[rb], Nb[rb], v[rb] + 4, bb);
+            bits[rb] = ba | (bb << 8);
+          }
+        } else {
         feature_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
                        Na[1], ja[0], ja[1]);
         piece(std::integral_constant<int, 1>{});
@@ -721,14 +797,23 @@ struct Producer {
           sparse8(jb[rb], Nb[rb], v[rb] + 4, bb);
           bits[rb] = ba | (bb << 8);
         }
+        }
       } else {
         float N[2][4];
         int jj[2];
-        feature_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
-                       jj[1]);
-        piece(std::integral_constant<int, 1>{});
+        if (cardinal) {
+          cardinal_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
+                          jj[1]);
+          piece(std::integral_constant<int, 1>{});
 #pragma unroll
-        for (int rb = 0; rb < 2; ++rb) sparse16(jj[rb], N[rb], v[rb], bits[rb]);
+          for (int rb = 0; rb < 2; ++rb) sparse16w(jj[rb], N[rb], v[rb], bits[rb]);
+        } else {
+          feature_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
+                         jj[1]);
+          piece(std::integral_constant<int, 1>{});
+#pragma unroll
+          for (int rb = 0; rb < 2; ++rb) sparse16(jj[rb], N[rb], v[rb], bits[rb]);
+        }
         piece(std::integral_constant<int, 2>{});
       }
     }
@@ -1009,9 +1094,14 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
       p.rlo = make_rsrc(blo, wbytes);
       p.rx = make_rsrc(x, (size_t)B * I * 4);
       p.rt = make_rsrc(tables, (size_t)ngroups * p.tgb);
-      bool ok = true;
-      for (int i = lane; i < nflags; i += kWave) ok = ok && uflags[i] != 0;
+      bool ok = true, card = true;
+      for (int i = lane; i < nflags; i += kWave) {
+        ok = ok && (uflags[i] & 1) != 0;
+        card = card && (uflags[i] & 2) != 0;
+      }
       p.uniform = __builtin_amdgcn_ballot_w64(!ok) == 0;
+      p.cardinal = __builtin_amdgcn_ballot_w64(!card) == 0;
+      p.C = L - 1 - kOrder;
       p.run();
     }
     wait_vmcnt<0>();  // no copy may still be writing LDS past this point
