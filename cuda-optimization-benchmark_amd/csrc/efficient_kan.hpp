@@ -4,26 +4,27 @@
 //   out[b,o] = sum_i silu(x[b,i]) Wb[o,i] + sum_i sum_c B_c(x[b,i]) Ws[o,i,c] sc[o,i]
 // with B_c the order-p B-spline bases on feature i's knot row (Cox-de Boor).
 //
-// One contraction over K = I * (1 + C') (C' = C rounded up to 8 or 16) on the fp16 MFMA
-// v_mfma_f32_16x16x32_f16 with a three-term split for fp32-level accuracy: every operand v
-// is carried as hi = fp16(v) and lo = fp16(v - hi), and each product as hi*hi + lo*hi +
-// hi*lo (the dropped lo*lo term is ~2^-22 relative), accumulated in fp32.
+// One contraction over K = I * (1 + C') (C' = C rounded up to 8 or 16) with a three-term
+// split for fp32-level accuracy: every operand v is carried as hi = fp16(v) and
+// lo = fp16(v - hi), and each product as hi*hi + lo*hi + hi*lo (the dropped lo*lo term is
+// ~2^-22 relative), accumulated in fp32.  The activations are the MFMAs' A operand and the
+// weights the B operand.
 //
-// K order: features in groups of 32; each group is one "silu" chunk (32 features, k =
-// feature) followed by C' "spline" chunks; spline chunk t holds the C' bases of the 32/C'
-// features i*C' + t (k = i*C' + basis).  In MFMA layout lane l supplies k = 8*(l/16) .. +7
-// of batch row l % 16, so over one group a lane needs x at one contiguous run of C'
-// features, and in a spline chunk it owns one (row, feature) and 8 of its bases: it finds
-// x's knot interval, evaluates the four bases nonzero there from per-interval cubic
-// coefficients and shifts them into its 8 slots.
+// K order (spline_k): features in groups of 32; each group is one silu chunk (32 features,
+// k = feature), contracted with the dense v_mfma_f32_16x16x32_f16, then C'/2 spline steps
+// of 64 k.  A feature has at most four nonzero bases (the window j-3 .. j of x's knot
+// interval j), and its bases are ordered so that every group of 4 k holds at most two of
+// them, so the spline activations are 2:4-sparse and each step is one
+// v_smfmac_f32_16x16x64_f16 per product term: a lane stores the 8 nonzero-or-paired values
+// of its 16 k with 2-bit positions, and its rows' bases come from the knot row (cardinal
+// cubic pieces on uniform rows, else per-interval cubics from a table).
 //
 // Per call, two launches: kan_pack finds each output column's power-of-two scale (so
-// neither fp16 half under- or overflows), writes the weights ([Wb | Ws*sc], the A operand)
-// in that K order as scaled fp16 hi/lo, [chunk][column][32] so each chunk's tile is
-// contiguous, and tabulates every feature's knot row and per-interval basis cubics;
-// kan_fused is the warp-specialized GEMM (producer waves copy weight tiles and expand
-// activations into LDS, consumer waves run the MFMAs) and undoes the column scale in its
-// epilogue.
+// neither fp16 half under- or overflows), writes the weights ([Wb | Ws*sc]) in that K order
+// as scaled fp16 hi/lo, [chunk of 32 k][column][32] so each chunk's tile is contiguous, and
+// tabulates every feature's knot row and per-interval basis cubics; kan_fused is the
+// warp-specialized GEMM (producer waves copy weight half-tiles and expand activations into
+// LDS, consumer waves run the MFMAs) and undoes the column scale in its epilogue.
 #pragma once
 
 #include <utility>
@@ -151,15 +152,13 @@ constexpr double kUniformRel = 1e-3;   // direct interval lookup
 constexpr double kCardinalRel = 1e-5;  // cardinal pieces in place of the table's cubics
 
 // ---------------------------------------------------------------------------------------
-// Weight preparation, one launch (kan_pack): each output column's scale, the GEMM's A
+// Weight preparation, one launch (kan_pack): each output column's scale, the GEMM's weight
 // operand, and the basis tables.
 // bhi/blo: [nchunks][Opad][32] fp16; chunk q = g*(1+Cp) + sub; sub 0 holds Wb[o, 32g + s],
-// sub >= 1 holds (Ws*sc)[o, f, c] with f = 32g + (s/Cp)*Cp + (sub-1), c = s % Cp (zero
-// past I, O or C), all times 2^e.  So over a group's spline chunks the lanes that supply
-// slots s..s+7 of a chunk walk the features (s/Cp)*Cp .. +Cp-1: the same 8 (Cp = 8) or 16
-// features whose silu values they supply, and the GEMM loads each lane's x values as one
-// contiguous run.  colscale[o] = 2^-e with e chosen so max|column| * 2^e is in
-// [2^14, 2^15), so neither fp16 half under- or overflows.
+// subs 1 .. Cp hold (Ws*sc)[o, f, c] at the place spline_k gives feature f % 32 of group g
+// and the basis order spline_basis (zero past I, O or C), all times 2^e.  colscale[o] =
+// 2^-e with e chosen so max|column| * 2^e is in [2^14, 2^15), so neither fp16 half under-
+// or overflows.
 // ---------------------------------------------------------------------------------------
 // The GEMM's K order within a feature group (32 features): chunk 0 holds silu(x) of the 32
 // features (k = feature); chunks 1 .. C' hold the spline bases, in C'/2 steps of 64 k (two
@@ -222,9 +221,9 @@ __device__ __forceinline__ void kan_tables_block(int block, const float* __restr
 // wave's loads cover 64 consecutive features of the column's contiguous rows.  Pass 1
 // reduces the column's max |w| over Wb, sc and Ws to colscale[o] (waves combine through
 // LDS); pass 2 reads the column again (now from the L2 or the Infinity Cache) and writes its
-// hi/lo weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots
-// (fl / Cp) * Cp .. in spline chunk 1 + fl % Cp of group f / 32 (fl = f % 32), and lanes
-// with fl < 4 also write silu slots 8 fl .. +7.  Workgroup tblocks also zeroes kan_fused's
+// hi/lo weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots at
+// spline_k(f % 32) in the permuted basis order, and lanes with f % 32 < 4 also write silu
+// slots 8 (f % 32) .. +7.  Workgroup tblocks also zeroes kan_fused's
 // split-K arrival counters (their place in the workspace moves with the shape, so every
 // call starts them from zero).
 constexpr int kPackCols = 2;
