@@ -546,17 +546,37 @@ __device__ __forceinline__ void sparse16(int j, const float (&N)[4], float* v, u
 // [0, 1): the cardinal cubic B-spline pieces (1-t)^3/6, t^3/2 - t^2 + 2/3,
 // -t^3/2 + t^2/2 + t/2 + 1/6 and t^3/6.  Bases outside [0, C) and x outside the knot span
 // give zero.
-__device__ __forceinline__ void cardinal_pieces(float t, int j, int C, bool inside, float (&P)[4]) {
+__device__ __forceinline__ void cardinal_pieces(float t, float (&P)[4]) {
   const float t2 = t * t, t3 = t2 * t, s = 1.0f - t;
   P[0] = s * s * s * (1.0f / 6.0f);
   P[1] = fmaf(0.5f, t3, 2.0f / 3.0f - t2);
   P[2] = fmaf(-0.5f, t3, fmaf(0.5f, t2 + t, 1.0f / 6.0f));
   P[3] = t3 * (1.0f / 6.0f);
+}
+
+__device__ __forceinline__ void mask_window(int j, int C, bool inside, float (&P)[4]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int b = j - 3 + i;
     P[i] = (inside && b >= 0 && b < C) ? P[i] : 0.0f;
   }
+}
+
+// A window needs neither the mask nor sparse_pair's clamping when x lies inside the knot
+// span and all four bases j-3 .. j exist (3 <= j <= C - 1).
+__device__ __forceinline__ bool window_whole(int j, int C, bool inside) { return inside && j >= 3 && j < C; }
+
+// sparse8w for a whole window (window_whole): the first even basis is 2 ((j - 2) >> 1) and
+// the first odd one 2 ((j - 3) >> 1) + 1, both pairs inside their groups, so the positions
+// need no clamping: the same values and bits as sparse8w.
+__device__ __forceinline__ void sparse8w_whole(int j, const float (&P)[4], float* v, unsigned& bits) {
+  const bool jo = (j & 1) != 0;
+  v[0] = jo ? P[0] : P[1];
+  v[1] = jo ? P[2] : P[3];
+  v[2] = jo ? P[1] : P[0];
+  v[3] = jo ? P[3] : P[2];
+  const unsigned fe = (unsigned)((j - 2) >> 1), fo = (unsigned)((j - 3) >> 1);
+  bits = (5u * fe + 4u) | ((5u * fo + 4u) << 4);  // p | (p + 1) << 2 per group
 }
 
 // sparse8 from the bases in window order (P[i] is basis j - 3 + i).
@@ -592,16 +612,16 @@ __device__ __forceinline__ void sparse16w(int j, const float (&P)[4], float* v, 
 // consumer lane's accumulator holds output column n0 + 64 w + 16 cb + lane % 16 of batch
 // rows m0 + 16 rb + 4 (lane / 16) + 0..3.
 //
-// Each product is hi*hi + lo*hi + hi*lo; a step is consumed in two phases: L (hi_a * lo_w)
-// then H (hi_a * hi_w, lo_a * hi_w), so a step's lo and hi weight planes are separate
-// half-tiles in a ring of three 32 KiB slots: half-tile 2s (lo of step s) and 2s + 1 (hi)
-// sit in slot (2s) % 3 and (2s + 1) % 3.  Barriers: A(s) before phase L of step s, B(s)
-// before its phase H.
-//   producers, between A(s) and B(s): copy lo(s+1) into the slot hi(s-1) left, refill the
-//     table set step s's features used, load the next group's x (at a group's silu step),
-//     evaluate row block 0 of step s+1's activations; wait for hi(s);
-//   between B(s) and A(s+1): copy hi(s+1) into the slot lo(s) left, evaluate row block 1,
-//     wait for lo(s+1) (and the table and x loads).
+// Each product is hi*hi + lo*hi + hi*lo; a step is consumed in two phases: H (hi_a * hi_w
+// and lo_a * hi_w) from the step's hi weight plane, then L (hi_a * lo_w) from its lo plane.
+// The planes are separate half-tiles in a ring of three 32 KiB slots: hi(s) and lo(s) sit in
+// slots (2s) % 3 and (2s + 1) % 3.  Barriers: A(s) publishes step s's activations and hi(s)
+// (phase H starts), B(s) publishes lo(s) and frees hi(s)'s slot (phase L starts).
+//   producers, between A(s) and B(s): refill the table set step s's features used, load the
+//     next group's x (at a group's silu step), copy hi(s+1) into the slot lo(s-1) left and
+//     evaluate the first part of step s+1's activations; wait for lo(s);
+//   between B(s) and A(s+1): copy lo(s+1) into hi(s)'s slot, finish the evaluation and
+//     write the activations; wait for hi(s+1), the table set and x.
 // Every copy has about one step to land.
 //
 // LDS (kLdsBytes): the ring (3 x 32 KiB: a half-tile is two 16 KiB sub-tiles, the chunks
@@ -728,29 +748,29 @@ struct Producer {
   // Both row blocks' bases of one feature on a cardinal knot row, in window order: the
   // knots t_0, t_1 read once for the two, then each row's interval knot t_j.
   __device__ __forceinline__ void cardinal_values(const float* fe, float x0, float x1, float (&P0)[4], float (&P1)[4],
-                                                  int& j0, int& j1) const {
+                                                  int& j0, int& j1, bool& in0, bool& in1) const {
     const f32x2 k01 = *reinterpret_cast<const f32x2*>(fe);
     const float inv_h = __builtin_amdgcn_rcpf(k01.y - k01.x);
     const int r0 = (int)__builtin_floorf((x0 - k01.x) * inv_h), r1 = (int)__builtin_floorf((x1 - k01.x) * inv_h);
     j0 = min(max(r0, 0), L - 2);
     j1 = min(max(r1, 0), L - 2);
     const float tj0 = fe[j0], tj1 = fe[j1];
-    cardinal_pieces((x0 - tj0) * inv_h, j0, C, r0 == j0, P0);
-    cardinal_pieces((x1 - tj1) * inv_h, j1, C, r1 == j1, P1);
+    in0 = r0 == j0;
+    in1 = r1 == j1;
+    cardinal_pieces((x0 - tj0) * inv_h, P0);
+    cardinal_pieces((x1 - tj1) * inv_h, P1);
   }
 
   // Step j's activations of a group, both of this wave's row blocks, into stage `st`: j = 0
   // the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline step
-  // u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).  The
-  // four pieces of step jc's plane of group lgc go out between the parts: a copy instruction
-  // holds the wave until the CU's memory pipeline takes it, so spreading them lets the
-  // evaluation's VALU work fill that time.
-  template <int kJ, int kJc, bool kCopy>
-  __device__ __forceinline__ void prepare(uint8_t* st, const float (&xs)[2][kX], __amdgpu_buffer_rsrc_t rp, int lgc,
-                                          int slot) const {
-    auto piece = [&](auto k) {
-      if constexpr (kCopy) copy_step_plane<kJc, decltype(k)::value, 4>(rp, lgc, slot);
-    };
+  // u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).
+  // `piece(k)`, k = 0 .. 3, runs once at each of four points spread through the evaluation
+  // (the step's copies and barrier B): a copy instruction holds the wave until the CU's
+  // memory pipeline takes it, so spreading them lets the evaluation's VALU work fill that
+  // time.  When every lane's windows are whole (x inside the knot span, all four bases in
+  // [0, C)), the wave packs without masks or position clamping.
+  template <int kJ, typename Piece>
+  __device__ __forceinline__ void prepare(uint8_t* st, const float (&xs)[2][kX], Piece piece) const {
     float v[2][8];
     unsigned bits[2] = {0u, 0u};
     piece(std::integral_constant<int, 0>{});
@@ -769,18 +789,33 @@ struct Producer {
         float Na[2][4], Nb[2][4];
         int ja[2], jb[2];
         if (cardinal) {
+          bool ia[2], ib[2];
           cardinal_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
-                          Na[1], ja[0], ja[1]);
+                          Na[1], ja[0], ja[1], ia[0], ia[1]);
           piece(std::integral_constant<int, 1>{});
           cardinal_values(reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), xs[0][2 * u + 1],
-                          xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1]);
+                          xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1], ib[0], ib[1]);
           piece(std::integral_constant<int, 2>{});
+          const bool whole = window_whole(ja[0], C, ia[0]) && window_whole(ja[1], C, ia[1]) &&
+                             window_whole(jb[0], C, ib[0]) && window_whole(jb[1], C, ib[1]);
+          if (__builtin_amdgcn_ballot_w64(!whole) == 0) {  // the whole wave: no masks, no clamping
 #pragma unroll
-          for (int rb = 0; rb < 2; ++rb) {
-            unsigned ba, bb;
-            sparse8w(ja[rb], Na[rb], v[rb], ba);
-            sparse8w(jb[rb], Nb[rb], v[rb] + 4, bb);
-            bits[rb] = ba | (bb << 8);
+            for (int rb = 0; rb < 2; ++rb) {
+              unsigned ba, bb;
+              sparse8w_whole(ja[rb], Na[rb], v[rb], ba);
+              sparse8w_whole(jb[rb], Nb[rb], v[rb] + 4, bb);
+              bits[rb] = ba | (bb << 8);
+            }
+          } else {
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) {
+              unsigned ba, bb;
+              mask_window(ja[rb], C, ia[rb], Na[rb]);
+              mask_window(jb[rb], C, ib[rb], Nb[rb]);
+              sparse8w(ja[rb], Na[rb], v[rb], ba);
+              sparse8w(jb[rb], Nb[rb], v[rb] + 4, bb);
+              bits[rb] = ba | (bb << 8);
+            }
           }
         } else {
         feature_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
@@ -801,9 +836,15 @@ struct Producer {
         float N[2][4];
         int jj[2];
         if (cardinal) {
+          bool in[2];
           cardinal_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
-                          jj[1]);
+                          jj[1], in[0], in[1]);
           piece(std::integral_constant<int, 1>{});
+          const bool whole = window_whole(jj[0], C, in[0]) && window_whole(jj[1], C, in[1]);
+          if (__builtin_amdgcn_ballot_w64(!whole) != 0) {  // some lane's window needs the mask
+#pragma unroll
+            for (int rb = 0; rb < 2; ++rb) mask_window(jj[rb], C, in[rb], N[rb]);
+          }
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) sparse16w(jj[rb], N[rb], v[rb], bits[rb]);
         } else {
@@ -861,12 +902,26 @@ struct Producer {
 #pragma unroll
           for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
       }
-      // hi(s+1), in pieces between the parts of step s+1's activations
-      prepare<kNJ, kNJ, true>(st, xcur, rhi, lgn, (2 * (s + 1)) % kSlots);
+      // Step s+1's activations are evaluated across both of the consumers' phases: hi(s+1)
+      // goes out in halves at points 0 and 1, B(s) sits at point 2, and lo(s+1) goes out in
+      // halves at points 2 and 3.
+      const int shi = (2 * (s + 1)) % kSlots, slo = (2 * (s + 1) + 1) % kSlots;
+      prepare<kNJ>(st, xcur, [&](auto k) {
+        constexpr int kk = decltype(k)::value;
+        if constexpr (kk < 2) {
+          copy_step_plane<kNJ, kk, 2>(rhi, lgn, shi);
+        } else {
+          if constexpr (kk == 2) {
+            wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
+            barrier_no_vm_drain();        // B(s)
+          }
+          copy_step_plane<kNJ, kk - 2, 2>(rlo, lgn, slo);
+        }
+      });
+    } else {
+      wait_vmcnt<kT + kXn>();  // lo(s) has landed
+      barrier_no_vm_drain();   // B(s)
     }
-    wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
-    barrier_no_vm_drain();        // B(s)
-    if constexpr (kNext) copy_step_plane<kNJ>(rlo, lgn, (2 * (s + 1) + 1) % kSlots);
     wait_vmcnt<kC>();             // hi(s+1), the table set and x have landed
     barrier_no_vm_drain();        // A(s+1)
   }
@@ -887,7 +942,7 @@ struct Producer {
     if (kS > 1) copy_table_set(0, 1);
     load_x(0, xcur);
     wait_vmcnt<0>();
-    prepare<0, 0, false>(smem + kActAt, xcur, rhi, 0, 0);
+    prepare<0>(smem + kActAt, xcur, [](auto) {});
     barrier_no_vm_drain();  // A(0)
     for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, std::make_integer_sequence<int, kQ>{});
     group_steps<true>(nlg - 1, xcur, xnext, std::make_integer_sequence<int, kQ>{});
