@@ -619,9 +619,9 @@ __device__ __forceinline__ void sparse16w(int j, const float (&P)[4], float* v, 
 // (phase H starts), B(s) publishes lo(s) and frees hi(s)'s slot (phase L starts).
 //   producers, between A(s) and B(s): refill the table set step s's features used, load the
 //     next group's x (at a group's silu step), copy hi(s+1) into the slot lo(s-1) left and
-//     evaluate the first part of step s+1's activations; wait for lo(s);
-//   between B(s) and A(s+1): copy lo(s+1) into hi(s)'s slot, finish the evaluation and
-//     write the activations; wait for hi(s+1), the table set and x.
+//     evaluate, pack and split step s+1's activations; wait for lo(s);
+//   between B(s) and A(s+1): copy lo(s+1) into hi(s)'s slot and write the activations; wait
+//     for hi(s+1), the table set and x.
 // Every copy has about one step to land.
 //
 // LDS (kLdsBytes): the ring (3 x 32 KiB: a half-tile is two 16 KiB sub-tiles, the chunks
@@ -903,21 +903,21 @@ struct Producer {
           for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
       }
       // Step s+1's activations are evaluated across both of the consumers' phases: hi(s+1)
-      // goes out in halves at points 0 and 1, B(s) sits at point 2, and lo(s+1) goes out in
-      // halves at points 2 and 3.
+      // goes out in halves at points 0 and 1, B(s) sits at point 3 (the values are packed
+      // and split by then: the consumers' phase H is the longer one), and lo(s+1) goes out
+      // in halves after B(s) and after the activation stores.
       const int shi = (2 * (s + 1)) % kSlots, slo = (2 * (s + 1) + 1) % kSlots;
       prepare<kNJ>(st, xcur, [&](auto k) {
         constexpr int kk = decltype(k)::value;
         if constexpr (kk < 2) {
           copy_step_plane<kNJ, kk, 2>(rhi, lgn, shi);
-        } else {
-          if constexpr (kk == 2) {
-            wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
-            barrier_no_vm_drain();        // B(s)
-          }
-          copy_step_plane<kNJ, kk - 2, 2>(rlo, lgn, slo);
+        } else if constexpr (kk == 3) {
+          wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
+          barrier_no_vm_drain();        // B(s)
+          copy_step_plane<kNJ, 0, 2>(rlo, lgn, slo);
         }
       });
+      copy_step_plane<kNJ, 1, 2>(rlo, lgn, slo);
     } else {
       wait_vmcnt<kT + kXn>();  // lo(s) has landed
       barrier_no_vm_drain();   // B(s)
