@@ -59,18 +59,15 @@ constexpr int BM = 128;
 constexpr int BN = 256;
 constexpr int kRB = BM / 16;                        // row blocks per tile (consumer)
 constexpr int kCB = BN / 16 / kConsumerWaves;       // column blocks per consumer wave
-constexpr int kSubTileBytes = BN * kChunk * 2;      // one plane (hi or lo) of one 32-k chunk: 16 KiB
-constexpr int kSlotBytes = 2 * kSubTileBytes;       // a half-tile: one plane of a 64-k step
-constexpr int kSlots = 3;                           // half-tile ring
 constexpr int kActFragBytes = kRB * 2 * 64 * 16;    // hi + lo activation fragments: 16 KiB
 constexpr int kActIdxBytes = kRB * 64 * 4;          // sparse positions: 2 KiB
 constexpr int kActBytes = kActFragBytes + kActIdxBytes;
 constexpr int kActStages = 2;
-constexpr int kActAt = kSlots * kSlotBytes;
+constexpr int kActAt = 0;
 constexpr int kTblAt = kActAt + kActStages * kActBytes;
 constexpr int kTblSetSlots = 8;                     // features per table set (C' = 8; C' = 16 uses 4)
 constexpr int kTblBytes = 2 * kTblSetSlots * 64 * kMaxKnots;  // two sets of 1 KiB entries: 16 KiB
-constexpr int kLdsBytes = kTblAt + kTblBytes;       // 148 KiB
+constexpr int kLdsBytes = kTblAt + kTblBytes;       // 52 KiB
 static_assert(kLdsBytes <= 160 * 1024, "fits one CU's LDS");
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, size_t bytes) {
@@ -391,15 +388,6 @@ __global__ __launch_bounds__(kPackThreads) void kan_pack(
   }
 }
 
-// ---------------------------------------------------------------------------------------
-// Weight tiles: 64-byte rows (32 fp16 of k); chunk c of row r sits at chunk c ^ ((r >> 1)
-// & 3), which spreads the 16 rows x 4 chunks of one fragment read over all banks
-// (measured on MI355X: 141 B/clk/CU against 127 unswizzled or with (r >> 2) & 3).
-__device__ __forceinline__ int swz_w(int row) { return (row >> 1) & 3; }
-__device__ __forceinline__ int swizzle64(int row, int chunk) {
-  return row * 64 + ((chunk ^ swz_w(row)) << 4);
-}
-
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
@@ -614,57 +602,30 @@ __device__ __forceinline__ void sparse16w(int j, const float (&P)[4], float* v, 
 //
 // Each product is hi*hi + lo*hi + hi*lo; a step is consumed in two phases: H (hi_a * hi_w
 // and lo_a * hi_w) from the step's hi weight plane, then L (hi_a * lo_w) from its lo plane.
-// The planes are separate half-tiles in a ring of three 32 KiB slots: hi(s) and lo(s) sit in
-// slots (2s) % 3 and (2s + 1) % 3.  Barriers: A(s) publishes step s's activations and hi(s)
-// (phase H starts), B(s) publishes lo(s) and frees hi(s)'s slot (phase L starts).
-//   producers, between A(s) and B(s): refill the table set step s's features used, load the
-//     next group's x (at a group's silu step), copy hi(s+1) into the slot lo(s-1) left and
-//     evaluate, pack and split step s+1's activations; wait for lo(s);
-//   between B(s) and A(s+1): copy lo(s+1) into hi(s)'s slot and write the activations; wait
-//     for hi(s+1), the table set and x.
-// Every copy has about one step to land.
+// A consumer wave is the only reader of its 64 weight columns, so it loads its weight
+// fragments straight into registers, a phase ahead: lo(s) during phase H(s), hi(s+1) during
+// phase L(s).  One barrier per step: A(s) publishes step s's activations (and tells the
+// producers the consumers are done with step s-1's stage).
+//   producers, between A(s) and A(s+1): refill the table set step s's features used, load
+//     the next group's x (at a group's silu step), evaluate, pack and split step s+1's
+//     activations and write them to stage (s+1) % 2; wait for the table set and x.
 //
-// LDS (kLdsBytes): the ring (3 x 32 KiB: a half-tile is two 16 KiB sub-tiles, the chunks
-// 2u+1 and 2u+2 of spline step u, 256 rows x 64 B each, swizzle64; the silu step uses one);
-// 2 activation stages of 18 KiB ([row block][hi, lo][lane] x 16 B, then the positions
-// [row block][lane] x 4 B); and the basis-table window, two sets of 8 (C' = 8) or 4
-// (C' = 16) feature entries: spline step u's features in set u % 2.
+// LDS (kLdsBytes): 2 activation stages of 18 KiB ([row block][hi, lo][lane] x 16 B, then
+// the positions [row block][lane] x 4 B) and the basis-table window, two sets of 8 (C' = 8)
+// or 4 (C' = 16) feature entries: spline step u's features in set u % 2.
 // ---------------------------------------------------------------------------------------
-
-// Half-tile plane `rp` of the step whose first chunk is q (one sub-tile, or two for a spline
-// step) into ring slot `slot`: copying wave `part` copies the 16-row groups 4 part ..
-// 4 part + 3 of each sub-tile.  A direct-to-LDS instruction writes 64 consecutive 16-byte
-// slots (16 rows of 64 bytes); lane i fetches the chunk the swizzle places in slot i.
-constexpr int kSubTileCopies = BN / 16 / 4;  // 1 KiB copies per copying wave per sub-tile
-template <int kSub, int kPiece = 0, int kPieces = 1>
-__device__ __forceinline__ void copy_half_tile(uint8_t* smem, __amdgpu_buffer_rsrc_t rp, int slot, int q, int Opad,
-                                               int n0, int part, int lane) {
-  uint8_t* st = smem + slot * kSlotBytes;
-  const int r16 = lane / 4, logical = (lane % 4) ^ swz_w(r16);  // groups are 16-row aligned
-  constexpr int kAll = kSub * kSubTileCopies, kPer = kAll / kPieces;
-#pragma unroll
-  for (int n = kPiece * kPer; n < (kPiece + 1) * kPer; ++n) {
-      const int t = n / kSubTileCopies, i = n % kSubTileCopies;
-      const int group = part * kSubTileCopies + i;
-      const unsigned off = (unsigned)(((size_t)(q + t) * Opad + n0 + group * 16 + r16) * 64 + 16 * logical);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rp, (__attribute__((address_space(3))) void*)(st + t * kSubTileBytes + group * 1024), 16, off, 0, 0, 0);
-    }
-}
 
 template <int kCp, bool kVec>
 struct Producer {
   static constexpr int kS = kCp / 2;                       // spline steps per group
   static constexpr int kQ = 1 + kS;                        // steps per group
-  static constexpr int kChunksPerGroup = 1 + kCp;
   static constexpr int kX = 8;                             // x values per row block per group
   static constexpr int kSetFeat = kCp == 8 ? 8 : 4;        // features per table set
   static constexpr int kTableCopies = kSetFeat / 4;        // per producer wave per set
-  static constexpr int kXLoads = kVec ? 2 * kX / 4 : 2 * kX;
 
   uint8_t* smem;
-  __amdgpu_buffer_rsrc_t rhi, rlo, rx, rt;
-  int I, L, B, Opad, n0;
+  __amdgpu_buffer_rsrc_t rx, rt;
+  int I, L, B;
   int g0, nlg;
   int lane, fr, fq, pw;
   int row[2];      // this lane's batch rows (global) for its two row blocks
@@ -672,14 +633,6 @@ struct Producer {
   bool cardinal;   // every knot row is uniform to 1e-5 h: cardinal pieces, no table cubics
   int C;           // bases per feature
   int tgb;
-
-  // Half-tiles of step s = lg * kQ + j (j = 0: silu, one sub-tile).
-  template <int kJ, int kPiece = 0, int kPieces = 1>
-  __device__ __forceinline__ void copy_step_plane(__amdgpu_buffer_rsrc_t rp, int lg, int slot) const {
-    const int q = (g0 + lg) * kChunksPerGroup + (kJ == 0 ? 0 : 2 * kJ - 1);
-    copy_half_tile<kJ == 0 ? 1 : 2, kPiece, kPieces>(smem, rp, slot, q, Opad, n0, pw, lane);
-    __builtin_amdgcn_sched_barrier(0);
-  }
 
   // The table entries of spline step u's features of group lg into set u % 2: this wave
   // copies the features of slots kTableCopies * pw ..; a feature's 64 L bytes are 4 L lanes
@@ -764,24 +717,18 @@ struct Producer {
   // Step j's activations of a group, both of this wave's row blocks, into stage `st`: j = 0
   // the silu chunk (slots 8 fq .. 8 fq + 7 from the lane's 8 x values), else spline step
   // u = j - 1 (the lane's features 2u, 2u + 1 of its run for C' = 8, u for C' = 16).
-  // `piece(k)`, k = 0 .. 3, runs once at each of four points spread through the evaluation
-  // (the step's copies and barrier B): a copy instruction holds the wave until the CU's
-  // memory pipeline takes it, so spreading them lets the evaluation's VALU work fill that
-  // time.  When every lane's windows are whole (x inside the knot span, all four bases in
-  // [0, C)), the wave packs without masks or position clamping.
-  template <int kJ, typename Piece>
-  __device__ __forceinline__ void prepare(uint8_t* st, const float (&xs)[2][kX], Piece piece) const {
+  // When every lane's windows are whole (x inside the knot span, all four bases in [0, C)),
+  // the wave packs without masks or position clamping.
+  template <int kJ>
+  __device__ __forceinline__ void prepare(uint8_t* st, const float (&xs)[2][kX]) const {
     float v[2][8];
     unsigned bits[2] = {0u, 0u};
-    piece(std::integral_constant<int, 0>{});
     if constexpr (kJ == 0) {
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) v[rb][t] = silu(xs[rb][t]);
-        if (rb == 0) piece(std::integral_constant<int, 1>{});
       }
-      piece(std::integral_constant<int, 2>{});
     } else {
       constexpr int u = kJ - 1;
       const uint8_t* set = smem + kTblAt + (u % 2) * kSetFeat * 64 * L;
@@ -792,10 +739,8 @@ struct Producer {
           bool ia[2], ib[2];
           cardinal_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
                           Na[1], ja[0], ja[1], ia[0], ia[1]);
-          piece(std::integral_constant<int, 1>{});
           cardinal_values(reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), xs[0][2 * u + 1],
                           xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1], ib[0], ib[1]);
-          piece(std::integral_constant<int, 2>{});
           const bool whole = window_whole(ja[0], C, ia[0]) && window_whole(ja[1], C, ia[1]) &&
                              window_whole(jb[0], C, ib[0]) && window_whole(jb[1], C, ib[1]);
           if (__builtin_amdgcn_ballot_w64(!whole) == 0) {  // the whole wave: no masks, no clamping
@@ -820,10 +765,8 @@ struct Producer {
         } else {
         feature_values(reinterpret_cast<const float*>(set + (2 * fq) * 64 * L), xs[0][2 * u], xs[1][2 * u], Na[0],
                        Na[1], ja[0], ja[1]);
-        piece(std::integral_constant<int, 1>{});
         feature_values(reinterpret_cast<const float*>(set + (2 * fq + 1) * 64 * L), xs[0][2 * u + 1],
                        xs[1][2 * u + 1], Nb[0], Nb[1], jb[0], jb[1]);
-        piece(std::integral_constant<int, 2>{});
 #pragma unroll
         for (int rb = 0; rb < 2; ++rb) {
           unsigned ba, bb;
@@ -839,7 +782,6 @@ struct Producer {
           bool in[2];
           cardinal_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
                           jj[1], in[0], in[1]);
-          piece(std::integral_constant<int, 1>{});
           const bool whole = window_whole(jj[0], C, in[0]) && window_whole(jj[1], C, in[1]);
           if (__builtin_amdgcn_ballot_w64(!whole) != 0) {  // some lane's window needs the mask
 #pragma unroll
@@ -850,17 +792,14 @@ struct Producer {
         } else {
           feature_values(reinterpret_cast<const float*>(set + fq * 64 * L), xs[0][u], xs[1][u], N[0], N[1], jj[0],
                          jj[1]);
-          piece(std::integral_constant<int, 1>{});
 #pragma unroll
           for (int rb = 0; rb < 2; ++rb) sparse16(jj[rb], N[rb], v[rb], bits[rb]);
         }
-        piece(std::integral_constant<int, 2>{});
       }
     }
     f16x8 hi[2], lo[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) split8(v[rb], hi[rb], lo[rb]);
-    piece(std::integral_constant<int, 3>{});
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       const int frag = 2 * pw + rb;
@@ -871,23 +810,17 @@ struct Producer {
   }
 
   // Step s = lg * kQ + kJ (the consumers' phases of step s run meanwhile): see the
-  // schedule above.  kLast: lg is the workgroup's last group.  Every condition is a
-  // constant, so the waits count exactly the loads issued after the one awaited.
+  // schedule above.  kLast: lg is the workgroup's last group.
   template <bool kLast, int kJ>
   __device__ __forceinline__ void step(int lg, float (&xcur)[2][kX], float (&xnext)[2][kX]) const {
     const int s = lg * kQ + kJ;
     constexpr bool kNext = !kLast || kJ + 1 < kQ;        // step s + 1 exists
     constexpr int kNJ = (kJ + 1) % kQ;                   // its position in its group
-    constexpr int kPlane = kNJ == 0 ? kSubTileCopies : 2 * kSubTileCopies;
-    constexpr int kC = kNext ? kPlane : 0;               // copies of one of its planes
     // The table set step s (spline step kJ - 1) used is refilled for spline step kJ + 1,
     // of this group or the next.
     constexpr int kU2 = kJ + 1;
     constexpr bool kRefill = kJ >= 1 && (kU2 < kS || !kLast);
-    constexpr int kT = kRefill ? kTableCopies : 0;
     constexpr bool kXNext = kJ == 0 && !kLast;
-    constexpr int kXn = kXNext ? kXLoads : 0;
-    const int lgn = kJ + 1 < kQ ? lg : lg + 1;
     uint8_t* st = smem + kActAt + ((s + 1) & 1) * kActBytes;
 
     if constexpr (kRefill) {
@@ -902,28 +835,10 @@ struct Producer {
 #pragma unroll
           for (int t = 0; t < kX; ++t) xcur[rb][t] = xnext[rb][t];
       }
-      // Step s+1's activations are evaluated across both of the consumers' phases: hi(s+1)
-      // goes out in halves at points 0 and 1, B(s) sits at point 3 (the values are packed
-      // and split by then: the consumers' phase H is the longer one), and lo(s+1) goes out
-      // in halves after B(s) and after the activation stores.
-      const int shi = (2 * (s + 1)) % kSlots, slo = (2 * (s + 1) + 1) % kSlots;
-      prepare<kNJ>(st, xcur, [&](auto k) {
-        constexpr int kk = decltype(k)::value;
-        if constexpr (kk < 2) {
-          copy_step_plane<kNJ, kk, 2>(rhi, lgn, shi);
-        } else if constexpr (kk == 3) {
-          wait_vmcnt<kT + kXn + kC>();  // lo(s) has landed
-          barrier_no_vm_drain();        // B(s)
-          copy_step_plane<kNJ, 0, 2>(rlo, lgn, slo);
-        }
-      });
-      copy_step_plane<kNJ, 1, 2>(rlo, lgn, slo);
-    } else {
-      wait_vmcnt<kT + kXn>();  // lo(s) has landed
-      barrier_no_vm_drain();   // B(s)
+      prepare<kNJ>(st, xcur);
     }
-    wait_vmcnt<kC>();             // hi(s+1), the table set and x have landed
-    barrier_no_vm_drain();        // A(s+1)
+    wait_vmcnt<0>();          // the table set and x have landed
+    barrier_no_vm_drain();    // A(s+1)
   }
 
   template <bool kLast, int... kJs>
@@ -936,28 +851,23 @@ struct Producer {
     float xcur[2][kX], xnext[2][kX];
     // Prologue: step 0's two planes, the table sets of the first group's spline steps 0 and
     // 1, its x, and step 0's activations (silu); A(0) publishes them.
-    copy_step_plane<0>(rhi, 0, 0);
-    copy_step_plane<0>(rlo, 0, 1);
     copy_table_set(0, 0);
     if (kS > 1) copy_table_set(0, 1);
     load_x(0, xcur);
     wait_vmcnt<0>();
-    prepare<0>(smem + kActAt, xcur, [](auto) {});
+    prepare<0>(smem + kActAt, xcur);
     barrier_no_vm_drain();  // A(0)
     for (int lg = 0; lg + 1 < nlg; ++lg) group_steps<false>(lg, xcur, xnext, std::make_integer_sequence<int, kQ>{});
     group_steps<true>(nlg - 1, xcur, xnext, std::make_integer_sequence<int, kQ>{});
   }
 };
 
-// Consumer phases.  A step's weight fragments: lane (column fr of block cb, quarter fq)
-// reads k = 8 fq .. 8 fq + 7 of each sub-tile (the sparse B operand takes both, k and
-// k + 32 of the step).  Activation fragments of two row blocks are read during the previous
-// pair's MFMAs.
-__device__ __forceinline__ f16x8 wfrag(const uint8_t* sub, int wave, int cb, int lane) {
-  const int r = wave * (kCB * 16) + cb * 16 + lane % 16;
-  return __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(sub + swizzle64(r, lane / 16)));
-}
-
+// Consumer phases.  A consumer lane (column fr of block cb, quarter fq) holds its weight
+// fragments in registers: k = 8 fq .. 8 fq + 7 of each 32-k chunk (the sparse B operand
+// takes two chunks, k and k + 32 of the step).  They come straight from the packed planes
+// (one 1 KiB load per column block and chunk: 16 rows of 64 bytes); each consumer wave is
+// the only reader of its 64 columns, so the weights bypass the LDS.  Activation fragments
+// of two row blocks are read during the previous pair's MFMAs.
 typedef _Float16 f16x16 __attribute__((ext_vector_type(16)));
 
 __device__ __forceinline__ f16x16 join16(f16x8 a, f16x8 b) {
@@ -980,17 +890,13 @@ __device__ __forceinline__ void read_act(const uint8_t* ast, int lane, int rb, A
   }
 }
 
-// Phase L (kH false: hi_a * lo_w) or H (hi_a * hi_w, then lo_a * hi_w) of one step, from the
-// weight plane in `slot` and the activations in `ast`.
-template <bool kSparse, bool kH>
-__device__ __forceinline__ void consume_phase(const uint8_t* slot, const uint8_t* ast, int wave, int lane,
-                                              f32x4 (&acc)[kRB][kCB]) {
-  f16x8 w0[kCB], w1[kCB];
-#pragma unroll
-  for (int cb = 0; cb < kCB; ++cb) {
-    w0[cb] = wfrag(slot, wave, cb, lane);
-    if constexpr (kSparse) w1[cb] = wfrag(slot + kSubTileBytes, wave, cb, lane);
-  }
+// Phase L (kH false: hi_a * lo_w) or H (hi_a * hi_w, then lo_a * hi_w) of one step, with the
+// weight plane in w0 / w1 and the activations in `ast`.  `load(k)` runs at the start of
+// pair k (k = 0 .. 3): it loads column block k of another plane, whose loads go out among
+// the pair's MFMAs.
+template <bool kSparse, bool kH, typename Load>
+__device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x8 (&w1)[kCB], const uint8_t* ast,
+                                              int lane, f32x4 (&acc)[kRB][kCB], Load load) {
   ActPair cur;
   read_act<kH>(ast, lane, 0, cur);
   __builtin_amdgcn_sched_barrier(0);
@@ -998,6 +904,7 @@ __device__ __forceinline__ void consume_phase(const uint8_t* slot, const uint8_t
   constexpr int kReads = kH ? 6 : 4;  // LDS reads of a pair
 #pragma unroll
   for (int rb = 0; rb < kRB; rb += 2) {
+    load(rb / 2);
     ActPair nxt;
     if (rb + 2 < kRB) read_act<kH>(ast, lane, rb + 2, nxt);
 #pragma unroll
@@ -1018,7 +925,12 @@ __device__ __forceinline__ void consume_phase(const uint8_t* slot, const uint8_t
       for (int u = 0; u < kReads; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 8 * kTerms / kReads, 0);      // MFMAs
+        if (u == 0 || u == kReads / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 load
       }
+    } else {
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 4 * kTerms, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (rb + 2 < kRB) cur = nxt;
@@ -1029,23 +941,48 @@ template <int kCp>
 struct Consumer {
   static constexpr int kS = kCp / 2;
   static constexpr int kQ = 1 + kS;
+  static constexpr int kChunksPerGroup = 1 + kCp;
 
+  // Column block cb of this wave's fragments of plane rp, for the step at position kJ of
+  // group lg (w1: the step's second chunk, spline steps only).
   template <int kJ>
-  __device__ __forceinline__ void step(int s, int wave, int lane, f32x4 (&acc)[kRB][kCB]) const {
+  __device__ __forceinline__ void load_block(__amdgpu_buffer_rsrc_t rp, int lg, int cb, f16x8 (&w0)[kCB],
+                                             f16x8 (&w1)[kCB]) const {
+    const int q = (g0 + lg) * kChunksPerGroup + (kJ == 0 ? 0 : 2 * kJ - 1);
+    const int so = q * Opad * 64;
+    w0[cb] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, voff + cb * 1024, so, 0));
+    if constexpr (kJ > 0)
+      w1[cb] = __builtin_bit_cast(f16x8, __builtin_amdgcn_raw_buffer_load_b128(rp, voff + cb * 1024, so + Opad * 64, 0));
+  }
+
+  // Step s = lg * kQ + kJ: phase H from hi(s) (in h0 / h1) while lo(s) loads into l0 / l1,
+  // then phase L from lo(s) while hi(s+1) loads into h0 / h1, then A(s+1).  After the last
+  // step the hi loads re-read the current group (harmless), so every step has the same
+  // shape.
+  template <int kJ>
+  __device__ __forceinline__ void step(int lg, int lane, f32x4 (&acc)[kRB][kCB], f16x8 (&h0)[kCB], f16x8 (&h1)[kCB],
+                                       f16x8 (&l0)[kCB], f16x8 (&l1)[kCB]) const {
+    const int s = lg * kQ + kJ;
+    constexpr int kNJ = (kJ + 1) % kQ;
+    const bool next = kJ + 1 < kQ || lg + 1 < nlg;
+    const int lgn = kJ + 1 < kQ ? lg : (next ? lg + 1 : lg);
     const uint8_t* ast = smem + kActAt + (s & 1) * kActBytes;
-    consume_phase<(kJ > 0), true>(smem + ((2 * s) % kSlots) * kSlotBytes, ast, wave, lane, acc);
-    barrier_no_vm_drain();  // B(s)
-    consume_phase<(kJ > 0), false>(smem + ((2 * s + 1) % kSlots) * kSlotBytes, ast, wave, lane, acc);
+    consume_phase<(kJ > 0), true>(h0, h1, ast, lane, acc, [&](int k) { load_block<kJ>(rlo, lg, k, l0, l1); });
+    consume_phase<(kJ > 0), false>(l0, l1, ast, lane, acc, [&](int k) { load_block<kNJ>(rhi, lgn, k, h0, h1); });
     barrier_no_vm_drain();  // A(s+1)
   }
 
   template <int... kJs>
-  __device__ __forceinline__ void group(int lg, int wave, int lane, f32x4 (&acc)[kRB][kCB],
+  __device__ __forceinline__ void group(int lg, int lane, f32x4 (&acc)[kRB][kCB], f16x8 (&h0)[kCB],
+                                        f16x8 (&h1)[kCB], f16x8 (&l0)[kCB], f16x8 (&l1)[kCB],
                                         std::integer_sequence<int, kJs...>) const {
-    (step<kJs>(lg * kQ + kJs, wave, lane, acc), ...);
+    (step<kJs>(lg, lane, acc, h0, h1, l0, l1), ...);
   }
 
   uint8_t* smem;
+  __amdgpu_buffer_rsrc_t rhi, rlo;
+  int g0, nlg, Opad;
+  int voff;  // this lane's fragment in a chunk: row n0 + 64 wave + fr, bytes 16 fq ..
 };
 
 // Output of a consumer accumulator: consumer wave wq, row block rb, column block cb, lane
@@ -1137,15 +1074,12 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
     {
       Producer<kCp, kVec> p;
       p.smem = smem;
-      p.I = I; p.L = L; p.B = B; p.Opad = Opad; p.n0 = n0;
+      p.I = I; p.L = L; p.B = B;
       p.g0 = g0; p.nlg = nlg;
       p.lane = lane; p.fr = lane % 16; p.fq = lane / 16; p.pw = wave - kConsumerWaves;
       p.row[0] = m0 + 32 * p.pw + p.fr;
       p.row[1] = p.row[0] + 16;
       p.tgb = tbl_group_bytes(L);
-      const size_t wbytes = (size_t)ngroups * (1 + kCp) * Opad * kChunk * 2;
-      p.rhi = make_rsrc(bhi, wbytes);
-      p.rlo = make_rsrc(blo, wbytes);
       p.rx = make_rsrc(x, (size_t)B * I * 4);
       p.rt = make_rsrc(tables, (size_t)ngroups * p.tgb);
       bool ok = true, card = true;
@@ -1168,10 +1102,24 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
   for (int rb = 0; rb < kRB; ++rb)
 #pragma unroll
     for (int cb = 0; cb < kCB; ++cb) acc[rb][cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  barrier_no_vm_drain();  // A(0)
   Consumer<kCp> cons;
   cons.smem = smem;
-  for (int lg = 0; lg < nlg; ++lg) cons.group(lg, wave, lane, acc, std::make_integer_sequence<int, kQ>{});
+  {
+    const size_t wbytes = (size_t)ngroups * (1 + kCp) * Opad * kChunk * 2;
+    cons.rhi = make_rsrc(bhi, wbytes);
+    cons.rlo = make_rsrc(blo, wbytes);
+  }
+  cons.g0 = g0;
+  cons.nlg = nlg;
+  cons.Opad = Opad;
+  cons.voff = (n0 + wave * (kCB * 16) + lane % 16) * 64 + 16 * (lane / 16);
+  f16x8 h0[kCB], h1[kCB], l0[kCB], l1[kCB];
+#pragma unroll
+  for (int cb = 0; cb < kCB; ++cb) cons.template load_block<0>(cons.rhi, 0, cb, h0, h1);  // hi(0)
+  barrier_no_vm_drain();  // A(0)
+  for (int lg = 0; lg < nlg; ++lg)
+    cons.group(lg, lane, acc, h0, h1, l0, l1, std::make_integer_sequence<int, kQ>{});
+  wait_vmcnt<0>();  // the last step's (unused) loads
 
   if (nsplit > 1) {
     // This thread's 16-byte slots of the partial tile: (wave, rb, cb, lane), so every
