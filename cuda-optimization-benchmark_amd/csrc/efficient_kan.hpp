@@ -936,8 +936,9 @@ __device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x
     if (rb + 2 < kRB) {
 #pragma unroll
       for (int u = 0; u < kReads; ++u) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
-        __builtin_amdgcn_sched_group_barrier(0x008, 8 * kTerms / kReads, 0);      // MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x008, 8 * kTerms / kReads - 1, 0);  // MFMAs
         if (u == 0 || u == kReads / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 load
       }
     } else if constexpr (kH) {
