@@ -898,9 +898,9 @@ __device__ __forceinline__ void read_act(const uint8_t* ast, int lane, int rb, A
 // at its start, so they have the whole phase to land.  During its last pair, phase H reads
 // phase L's first pair into `lfirst`; phase L, once that pair's activations are in
 // registers, arrives at A(s+1) and then reads the next step's first pair (stage
-// `ast_next`, just published) into `lfirst`.  The scheduling groups keep one-load slots
-// among the MFMAs (0x020, now empty: the loads go out earlier); without them the compiler's
-// order measured about 1 % slower.
+// `ast_next`, just published) into `lfirst`.  The first pair's schedule places the
+// phase's loads after its first MFMA and LDS read (measured about 1 % faster than before
+// them).
 template <bool kSparse, bool kH, typename Load>
 __device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x8 (&w1)[kCB], const uint8_t* ast,
                                               int lane, f32x4 (&acc)[kRB][kCB], Load load, ActPair cur,
@@ -939,21 +939,21 @@ __device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        // MFMA
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 8 * kTerms / kReads - 1, 0);  // MFMAs
-        if (u == 0 || u == kReads / 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 load
+        if (u == 0) __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // the loads
       }
     } else if constexpr (kH) {
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * kTerms, 0);               // MFMAs
-        if (u == 0 || u == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 load
+        if (u == 0 || u == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // empty load slot (kept: measured faster)
       }
     } else {
 #pragma unroll
       for (int u = 0; u < 6; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        // MFMA
-        if (u == 0 || u == 3) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 load
+        if (u == 0 || u == 3) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // empty load slot (kept: measured faster)
       }
     }
     __builtin_amdgcn_sched_barrier(0);
