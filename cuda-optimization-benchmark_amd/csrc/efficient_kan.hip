@@ -82,7 +82,7 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
   const int table_blocks = (ngroups * kGroup * L + kPackThreads - 1) / kPackThreads;  // a thread per entry
-  // Split-K when the output tiles leave CUs idle (one workgroup fills a CU's LDS): up to
+  // Split-K when the output tiles leave CUs idle (one workgroup fills a CU's registers): up to
   // CUs / tiles splits of the feature groups, none empty.
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
   int nsplit = 1, gper = ngroups;

@@ -23,8 +23,9 @@
 // neither fp16 half under- or overflows), writes the weights ([Wb | Ws*sc]) in that K order
 // as scaled fp16 hi/lo, [chunk of 32 k][column][32] so each chunk's tile is contiguous, and
 // tabulates every feature's knot row and per-interval basis cubics; kan_fused is the
-// warp-specialized GEMM (producer waves copy weight half-tiles and expand activations into
-// LDS, consumer waves run the MFMAs) and undoes the column scale in its epilogue.
+// warp-specialized GEMM (producer waves expand the activations into LDS, consumer waves
+// load their weight fragments straight into registers and run the MFMAs) and undoes the
+// column scale in its epilogue.
 #pragma once
 
 #include <utility>
@@ -49,10 +50,10 @@ constexpr unsigned kOutOfRange = 0x80000000u;
 
 // kan_fused tiling: a 128 x 256 output tile per workgroup of 8 waves.  Waves 0-3 are
 // consumers: wave w owns all 128 batch rows (8 row blocks of 16) x output columns
-// 64w .. 64w+63 (4 column blocks), 128 fp32 accumulators, and only reads LDS and issues
-// MFMAs.  Waves 4-7 are producers: producer p copies a quarter of each weight half-tile
-// into LDS and expands the activations of batch rows 32p .. 32p+31 (2 row blocks).  One
-// producer and one consumer share each SIMD.
+// 64w .. 64w+63 (4 column blocks), 128 fp32 accumulators; it loads its weight fragments,
+// reads the activations from LDS and issues the MFMAs.  Waves 4-7 are producers: producer
+// p expands the activations of batch rows 32p .. 32p+31 (2 row blocks).  One producer and
+// one consumer share each SIMD.
 constexpr int kThreads = 512;
 constexpr int kConsumerWaves = 4;
 constexpr int BM = 128;
