@@ -8,7 +8,8 @@ the torch.ops.taskops operators (libtaskops_torch.so, g++), in-tree under `lib/`
 The drop-in libraries (`lib/dropin_<op>.so`) each hold the C++ `void reference(...)`
 overload of one task plus the grader's `extern "C" void grader_entry(void**)` shim,
 linked against libtaskops.so, so the reference benchmark's ctypes driver
-(graders/child.py:79-100) can load one per task unchanged.
+(graders/child.py:79-100) can load one per task unchanged.  `lib/planted_<op>.so` is the
+same entry with planted faults (grader/plants.py), the harness's negative controls.
 """
 from __future__ import annotations
 
@@ -83,6 +84,15 @@ def dropin_source(op: str) -> str:
     return shim(parse(load_task(op)["hip_signature"]))
 
 
+def planted_source(op: str) -> str:
+    """The planted-control variant of an op's drop-in (grader/plants.py)."""
+    from .grader.plants import planted_source as source
+    from .grader.signature import parse
+    from .tasks import load_task
+    task = load_task(op)
+    return source(parse(task["hip_signature"]), task["outputs"])
+
+
 def build(verbose: bool = True, jobs: int | None = None) -> Path:
     """Compile every HIP source for gfx950 and link lib/libtaskops.so plus the drop-ins."""
     if shutil.which(HIPCC) is None and not Path(HIPCC).exists():
@@ -97,24 +107,27 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     _run([HIPCC, *COMMON, "-shared", "-o", str(tmp), *map(str, objs), "-Wl,-Bsymbolic"])
     os.replace(tmp, lib)
 
-    def _dropin(op: str) -> Path:
-        src = OBJ / f"dropin_{op}.hip"
-        src.write_text(dropin_source(op))
-        out = LIB / f"dropin_{op}.so"
-        t = LIB / f"dropin_{op}.so.tmp"
+    def _entry(name: str, text: str) -> Path:
+        src = OBJ / f"{name}.hip"
+        src.write_text(text)
+        out = LIB / f"{name}.so"
+        t = LIB / f"{name}.so.tmp"
         _run([HIPCC, *COMMON, "-shared", "-o", str(t), str(src), f"-L{LIB}", "-ltaskops",
               "-Wl,-rpath,$ORIGIN", "-Wl,-Bsymbolic"])
         os.replace(t, out)
         return out
 
+    entries = [(f"dropin_{op}", dropin_source(op)) for op in OPS] + \
+              [(f"planted_{op}", planted_source(op)) for op in OPS]
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        list(ex.map(_dropin, OPS))
+        list(ex.map(lambda e: _entry(*e), entries))
     counter = LIB / "libhipcount.so"
     _run([CC, *COUNTER_CFLAGS, str(CSRC / "callcount.c"), "-o", str(LIB / "libhipcount.so.tmp"), "-ldl"])
     os.replace(LIB / "libhipcount.so.tmp", counter)
     ext = build_torch_ops()
     if verbose:
-        print(f"built {lib}, {len(OPS)} drop-in libraries, {counter.name} and {ext.name}", flush=True)
+        print(f"built {lib}, {len(OPS)} drop-in and {len(OPS)} planted libraries, {counter.name} and {ext.name}",
+              flush=True)
     return lib
 
 

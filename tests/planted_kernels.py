@@ -10,6 +10,10 @@ Not collected by pytest.
   fill, a copy, an add), so the harness's device-side checks -- guard gaps, 0xFF
   outputs, unchanged inputs, call-2 results, repeat bits -- must catch it.  Every planted
   write lands inside the arena's one allocation; no GPU kernel is altered.
+- PlantedLibrary (GPU): the task's planted drop-in library, lib/planted_<op>.so
+  (grader/plants.py): the real entry with the fault compiled in, a HIP kernel launched
+  after it (or, for a cached result, a call that returns before launching anything),
+  reached through the same grader_entry ABI as the task's own library.
 """
 import numpy as np
 import torch
@@ -131,3 +135,23 @@ class DeviceFault:
                 kernel()
             _plant_after(self.fault, arena, self.task, calls, cache)
         return fire
+
+
+class PlantedLibrary:
+    """A GPU runner: lib/planted_<op>.so with `fault` selected.  One runner grades one case
+    (the library counts its calls from the selection, for the cached and call-3 kinds)."""
+
+    def __init__(self, op: str, fault: str | None = None):
+        import ctypes
+        from cob_amd import LIB_DIR
+        from cob_amd.grader.entry import DropInLibrary
+        from cob_amd.grader.plants import KINDS
+        path = LIB_DIR / f"planted_{op}.so"
+        self.lib = DropInLibrary(op, path=path)
+        select = ctypes.CDLL(str(path)).planted_select
+        select.argtypes = [ctypes.c_int]
+        select.restype = None
+        select(KINDS.index(fault or "none"))
+
+    def bind(self, arena, scalars):
+        return self.lib.bind(arena, scalars)

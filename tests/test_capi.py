@@ -1,5 +1,6 @@
 """The C ABI on the CPU: libtaskops.so loads and exports every symbol include/taskops.h
-declares; each drop-in library exports `grader_entry` and its C++ `reference` overload.
+declares; each drop-in library exports `grader_entry` and its C++ `reference` overload, and
+each planted library `grader_entry` and `planted_select`.
 No compute call is made (no GPU here)."""
 import ctypes
 import re
@@ -39,6 +40,14 @@ def test_dropin_exports(op):
     assert hasattr(lib, "grader_entry")
     dyn = subprocess.run(["nm", "-D", "-C", "--defined-only", str(p)], capture_output=True, text=True).stdout
     assert re.search(r"\breference\(", dyn), dyn
+
+
+@pytest.mark.parametrize("op", tasks.OPS)
+def test_planted_exports(op):
+    """The planted controls (grader/plants.py) share the drop-in ABI and add planted_select."""
+    p = LIB_DIR / f"planted_{op}.so"
+    lib = ctypes.CDLL(str(p))
+    assert hasattr(lib, "grader_entry") and hasattr(lib, "planted_select")
 
 
 def test_missing_library_fails_loudly(tmp_path):

@@ -12,7 +12,10 @@ planted run):
     input modified     one input byte changed on the device
     nonrepeatable      call 3 differs from call 1 in one bit (a pass, repeat bits false)
 
-No GPU kernel is altered: every plant is a torch device operation on the arena.
+test_device_plant_gets_its_label alters no GPU kernel: every plant is a torch device
+operation on the arena.  test_hip_plant_gets_its_label grades the planted drop-in libraries
+(lib/planted_<op>.so, grader/plants.py): the fault is a HIP kernel (or a skipped call)
+behind the task's grader_entry ABI, as the reference's planted kernels are CUDA builds.
 """
 import pytest
 
@@ -20,7 +23,7 @@ from cob_amd import tasks
 from cob_amd.grader.labels import kernel_status
 from cob_amd.grader.protocol import run_case
 from oracle import exact
-from planted_kernels import EXPECT, DeviceFault
+from planted_kernels import EXPECT, DeviceFault, PlantedLibrary
 
 pytestmark = pytest.mark.gpu
 
@@ -37,3 +40,14 @@ def test_device_plant_gets_its_label(lib, op, fault):
     st = kernel_status([[report]])
     assert (st["status"], st["label"]) == EXPECT[fault], (report["checks"], report["calls"])
     assert st["repeat_identical"] is (fault != "nonrepeatable")
+
+
+@pytest.mark.parametrize("fault", list(EXPECT))
+@pytest.mark.parametrize("op", tasks.OPS)
+def test_hip_plant_gets_its_label(lib, op, fault):
+    print(f"\n[planted lib] {op} {fault}", flush=True)
+    report = run_case(op, _public(op), exact.reference_exact, runner=PlantedLibrary(op, fault))
+    st = kernel_status([[report]])
+    assert (st["status"], st["label"]) == EXPECT[fault], (report["checks"], report["calls"])
+    # a library that skips its later calls leaves call 3's outputs unwritten as well
+    assert st["repeat_identical"] is (fault not in ("nonrepeatable", "cached_result"))
