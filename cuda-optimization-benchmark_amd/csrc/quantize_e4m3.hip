@@ -210,22 +210,30 @@ __global__ __launch_bounds__(kThreads) void qz_cast_any(const float* __restrict_
 // ---------------------------------------------------------------------------------------
 // Fused single pass.
 // ---------------------------------------------------------------------------------------
-// Barrier words in the workspace after the partials, one per 64-byte line: group g's
-// arrival count and max, the top count and max, the published result and the sense flag.
-// Arrival is two-level (RMWs on one address serialise at the coherence point, about 12 ns
-// each): workgroup b arrives in group b % 16; a group's last arrival folds the group max
-// into the top max and arrives at the top; the top's last arrival publishes the max and
-// flips the sense.  Workgroups wait for the sense to differ from what they read at start
-// (a sense-reversal barrier): the last arrivals reset every count and max on the way, and
-// the flipped sense is the next launch's starting value, so no host reset is needed and a
-// captured graph replays correctly.
+// Barrier words in the workspace after the partials, one per 64-byte line, in two sets;
+// the parity word says which set a launch uses.  Set s holds group g's arrival count and
+// max and the top arrival count.  RMWs on one address serialise at the coherence point
+// (about 12 ns each), so arrival is two-level: workgroup b folds its max into group b % 16's
+// max and then counts itself in the group (each RMW's result is used before the next is
+// issued, which orders them at the coherence point); a group's last arrival counts the group
+// in at the top.  The grid's last arrival clears the other set (the previous launch's, which
+// the next launch uses) and flips the parity.  Waiters poll the parity word, which no RMW
+// touches, until it differs from what they read at start, then read the group maxima, final
+// by then, and take their max: from the last arrival's data that is two RMWs, the group's
+// top RMW, the flip, one poll and one read.  A set is only cleared by the launch after the
+// one that reads it, every launch leaves the next one a cleared set, no host reset is needed
+// and a captured graph replays correctly.
 constexpr int kQzGroups = 16;
 constexpr int kQzLine = 16;  // unsigned per 64-byte line
-enum QzWord : int { kQzGroupCount = 0, kQzGroupMax = kQzGroups, kQzTopCount = 2 * kQzGroups, kQzTopMax,
-                    kQzResult, kQzSense, kQzWords };
-constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the sense flag (~0.5-1 us each) before the fallback
+enum QzWord : int { kQzGroupCount = 0, kQzGroupMax = kQzGroups, kQzTopCount = 2 * kQzGroups, kQzSetWords };
+constexpr int kQzParity = 2 * kQzSetWords;  // after both sets
+constexpr int kQzWords = kQzParity + 1;
+constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the parity (~0.5-1 us each) before the fallback
 
-__device__ __forceinline__ unsigned* qz_word(unsigned* bar, int w, int i = 0) { return bar + (w + i) * kQzLine; }
+__device__ __forceinline__ unsigned* qz_word(unsigned* bar, unsigned set, int w, int i = 0) {
+  return bar + ((int)set * kQzSetWords + w + i) * kQzLine;
+}
+__device__ __forceinline__ unsigned* qz_parity(unsigned* bar) { return bar + kQzParity * kQzLine; }
 __device__ __forceinline__ unsigned qz_load(unsigned* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -250,46 +258,47 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) v
   const int64_t base = (int64_t)blockIdx.x * kChunk;
   f32x4 v[kVecs];
   load_chunk(x, n, base, v);
-  // The sense is read behind the chunk's loads; it only has to be read before this
+  // The parity is read behind the chunk's loads; it only has to be read before this
   // workgroup arrives.
-  unsigned sense = 0u;
-  if (threadIdx.x == 0) sense = qz_load(qz_word(bar, kQzSense));
+  unsigned parity = 0u;
+  if (threadIdx.x == 0) parity = qz_load(qz_parity(bar));
   const unsigned m = block_max_u32(chunk_max(v, 0u), lds);
 
-  if (threadIdx.x == 0) {
-    asm volatile("" ::"v"(sense));
+  if (threadIdx.x < kWave) {  // wave 0 runs the barrier; lane 0 makes the RMWs
+    const int lane = threadIdx.x;
+    parity = (unsigned)__shfl((int)parity, 0, kWave);
+    const unsigned set = parity & 1u;
     const unsigned grid = gridDim.x, g = blockIdx.x % kQzGroups;
     const unsigned groups = grid < kQzGroups ? grid : kQzGroups;
     const unsigned members = grid / kQzGroups + (g < grid % kQzGroups ? 1u : 0u);
-    unsigned r = qz_max(qz_word(bar, kQzGroupMax, g), m);
-    asm volatile("" ::"v"(r));
-    if (qz_add(qz_word(bar, kQzGroupCount, g)) == members - 1) {  // the group's last arrival
-      const unsigned gm = qz_load(qz_word(bar, kQzGroupMax, g));
-      asm volatile("" ::"v"(gm));
-      qz_store(qz_word(bar, kQzGroupMax, g), 0u);
-      qz_store(qz_word(bar, kQzGroupCount, g), 0u);
-      r = qz_max(qz_word(bar, kQzTopMax), gm);
+    bool last = false;
+    if (lane == 0) {
+      const unsigned r = qz_max(qz_word(bar, set, kQzGroupMax, g), m);
       asm volatile("" ::"v"(r));
-      if (qz_add(qz_word(bar, kQzTopCount)) == groups - 1) {  // the grid's last arrival
-        const unsigned tm = qz_load(qz_word(bar, kQzTopMax));
-        r = __hip_atomic_exchange(qz_word(bar, kQzResult), tm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("" ::"v"(r));
-        qz_store(qz_word(bar, kQzTopMax), 0u);
-        qz_store(qz_word(bar, kQzTopCount), 0u);
-        r = __hip_atomic_exchange(qz_word(bar, kQzSense), sense ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        asm volatile("" ::"v"(r));
+      if (qz_add(qz_word(bar, set, kQzGroupCount, g)) == members - 1)  // the group's last arrival
+        last = qz_add(qz_word(bar, set, kQzTopCount)) == groups - 1;     // the grid's last arrival
+    }
+    if (__builtin_amdgcn_ballot_w64(last) != 0ull) {
+      if (lane < kQzSetWords) qz_store(qz_word(bar, set ^ 1u, 0, lane), 0u);
+      if (lane == 0) qz_store(qz_parity(bar), parity ^ 1u);
+    }
+    bool done = false;
+    if (lane == 0) {
+      for (unsigned i = 0; i < spin_limit; ++i) {
+        if (qz_load(qz_parity(bar)) != parity) {
+          done = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
     }
-    bool flipped = false;
-    for (unsigned i = 0; i < spin_limit; ++i) {
-      if (qz_load(qz_word(bar, kQzSense)) != sense) {
-        flipped = true;
-        break;
-      }
-      __builtin_amdgcn_s_sleep(2);
+    done = __builtin_amdgcn_ballot_w64(done) != 0ull;
+    unsigned gm = 0u;
+    if (done) gm = wave_max_u32((unsigned)lane < groups ? qz_load(qz_word(bar, set, kQzGroupMax, lane)) : 0u);
+    if (lane == 0) {
+      fallback_s = done ? 0u : 1u;
+      gmax_s = gm;
     }
-    fallback_s = flipped ? 0u : 1u;
-    gmax_s = flipped ? qz_load(qz_word(bar, kQzResult)) : 0u;
   }
   __syncthreads();
   unsigned gm = gmax_s;
