@@ -81,7 +81,9 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   const int nq = ngroups * (1 + kCp);
   const size_t half_bytes = (size_t)nq * Opad * kChunk * sizeof(_Float16);
   const size_t table_bytes = (size_t)ngroups * tbl_group_bytes(L);
-  const int table_blocks = (ngroups * kGroup * L + kPackThreads - 1) / kPackThreads;  // a thread per entry
+  // kan_pack: one workgroup per kPackThreads basis-table entries (L per feature), each
+  // writing one knot-row flag word, then one per column pair.
+  const int table_blocks = (ngroups * kGroup * L + kPackThreads - 1) / kPackThreads;
   // Split-K when the output tiles leave CUs idle (one workgroup fills a CU's registers): up to
   // CUs / tiles splits of the feature groups, none empty.
   const int tiles = ((B + BM - 1) / BM) * (Opad / BN);
@@ -107,8 +109,8 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   auto* partial = reinterpret_cast<float*>(static_cast<char*>(wsp) + partial_at);
   // One launch finds the column scales, packs the weights and builds the basis tables and
   // their uniform-grid flags.
-  hipLaunchKernelGGL(kan_pack<kCp>, dim3(table_blocks + Opad / kPackCols), dim3(kPackThreads), 0, stream, wb, ws,
-                     sc, I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags, counters,
+  hipLaunchKernelGGL(kan_pack<kCp>, dim3(Opad / kPackCols + table_blocks), dim3(kPackThreads), 0, stream, wb, ws, sc,
+                     I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags, counters,
                      nsplit > 1 ? tiles : 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;

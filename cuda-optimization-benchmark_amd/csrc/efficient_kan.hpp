@@ -97,6 +97,68 @@ __host__ __device__ inline int tbl_group_bytes(int L) { return 4096 * ((L + 1) /
 // at a 64-byte stride) hit different banks.
 __host__ __device__ inline int tbl_chunk(int j, int r) { return r ^ ((j >> 2) & 3); }
 
+// Whether a knot row is uniform to within rel: h > 0 and every knot within rel * h of
+// t_0 + k h.  Within 1e-3 h the GEMM's direct interval lookup is exact enough; within 1e-5 h
+// the bases are the cardinal cubic pieces to ~1e-5 of a basis value, so the GEMM may
+// evaluate those instead of the table's per-interval cubics (the grids efficient-kan builds,
+// arange * h + a in fp32, are uniform to a few ulps: ~1e-6 h).
+// The row is passed in registers (kn[k] for k < L) and the loops are unrolled with the
+// bound as a predicate, so the check is one pass of arithmetic; walking the row in memory
+// with an early exit made it a chain of dependent cache round trips.
+__host__ __device__ inline bool kan_knots_uniform(const float (&kn)[kMaxKnots], int L, double rel) {
+  if (L < 2) return false;
+  const double t0 = (double)kn[0];
+  double tl = t0;
+#pragma unroll
+  for (int k = 1; k < kMaxKnots; ++k)
+    if (k == L - 1) tl = (double)kn[k];
+  const double h = (tl - t0) / (L - 1);
+  if (!(h > 0.0) || !(h < 1e300)) return false;
+  bool ok = true;
+#pragma unroll
+  for (int k = 0; k < kMaxKnots; ++k)
+    if (k < L) ok = ok && __builtin_fabs((double)kn[k] - (t0 + k * h)) <= rel * h;
+  return ok;
+}
+constexpr double kUniformRel = 1e-3;   // direct interval lookup
+constexpr double kCardinalRel = 1e-5;  // cardinal pieces in place of the table's cubics
+
+// Spacing h of a knot row as the uniformity check defines it: (t_{L-1} - t_0) / (L - 1).
+__host__ __device__ inline double kan_row_spacing(const float (&kn)[kMaxKnots], int L) {
+  double tl = (double)kn[0];
+#pragma unroll
+  for (int k = 1; k < kMaxKnots; ++k)
+    if (k == L - 1) tl = (double)kn[k];
+  return (tl - (double)kn[0]) / (L - 1);
+}
+
+// Interval j's cubics for a knot row uniform to 1e-5 h (kan_knots_uniform with
+// kCardinalRel): on a uniform row every basis N_{k,3} with 0 <= k <= L - 5 is the cardinal
+// cubic B-spline, and on interval j basis j - 3 + r is its piece 3 - r, in t = u / h:
+//   piece 0  t^3 / 6                      piece 1  (1 + 3t + 3t^2 - 3t^3) / 6
+//   piece 2  (4 - 6t^2 + 3t^3) / 6        piece 3  (1 - t)^3 / 6
+// so the coefficient of u^c is the piece's coefficient of t^c times h^-c.  Against the fp64
+// recursion on the row's own knots (kan_table_entry) it differs by the row's deviation from
+// uniform, at most about 1e-5 of a basis value, the same approximation kan_fused makes when
+// it evaluates these pieces itself; it needs one division where the recursion needs 32.
+__host__ __device__ inline void kan_cardinal_entry(int L, int j, double h, float* __restrict__ dst) {
+  constexpr double kPiece[4][4] = {{0.0, 0.0, 0.0, 1.0 / 6.0},
+                                   {1.0 / 6.0, 0.5, 0.5, -0.5},
+                                   {2.0 / 3.0, 0.0, -1.0, 0.5},
+                                   {1.0 / 6.0, -0.5, 0.5, -1.0 / 6.0}};
+  const double ih = 1.0 / h;
+  const double ihp[4] = {1.0, ih, ih * ih, ih * ih * ih};
+#pragma unroll
+  for (int r = 0; r <= kOrder; ++r) {  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
+    const int kb = j - kOrder + r;
+    const bool exists = kb >= 0 && kb <= L - 2 - kOrder;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] =
+          exists ? (float)(kPiece[kOrder - r][c] * ihp[c]) : 0.0f;
+  }
+}
+
 // Entry j of a feature's table (dst: the feature's 16 * L floats): j = -1 writes the knot
 // row, j in [0, L-1) interval j's cubics.
 __host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, int L, int j, float* __restrict__ dst) {
@@ -104,50 +166,55 @@ __host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, in
     for (int k = 0; k < kMaxKnots; ++k) dst[k] = k < L ? knots_row[k] : __builtin_inff();
     return;
   }
-  double t[kMaxKnots];
-  for (int k = 0; k < kMaxKnots; ++k) t[k] = k < L ? (double)knots_row[k] : 0.0;
+  // The recursion for interval j only reads knots j-3 .. j+4; w[i] = t_{j-3+i} (0 outside the
+  // row, never read: the index ranges below keep k >= 0 and k + p + 1 <= L - 1).  With the
+  // loops unrolled every index into w, P and Q is a constant, so they stay in registers;
+  // indexing a whole knot row by the thread's j instead turned each access into a chain of
+  // selects over the row, and the table took 7-11 us of kan_pack's critical path.
+  double w[2 * (kOrder + 1)];
+#pragma unroll
+  for (int i = 0; i < 2 * (kOrder + 1); ++i) {
+    const int k = j - kOrder + i;
+    w[i] = (k >= 0 && k < L) ? (double)knots_row[k] : 0.0;
+  }
   double P[kOrder + 1][4];  // P[r]: N_{j-3+r, p} as a cubic in u
+#pragma unroll
   for (int r = 0; r <= kOrder; ++r)
+#pragma unroll
     for (int c = 0; c < 4; ++c) P[r][c] = 0.0;
-  if (t[j + 1] > t[j]) P[kOrder][0] = 1.0;  // N_{j,0} on [t_j, t_{j+1})
+  if (w[kOrder + 1] > w[kOrder]) P[kOrder][0] = 1.0;  // N_{j,0} on [t_j, t_{j+1})
+#pragma unroll
   for (int p = 1; p <= kOrder; ++p) {
     double Q[kOrder + 1][4];
+#pragma unroll
     for (int r = 0; r <= kOrder; ++r) {
+#pragma unroll
       for (int c = 0; c < 4; ++c) Q[r][c] = 0.0;
-      const int k = j - kOrder + r;
+      const int k = j - kOrder + r;  // t_k = w[r], t_j = w[kOrder]
       if (r < kOrder - p || k < 0 || k > L - 2 - p) continue;
-      const double d1 = t[k + p] - t[k], d2 = t[k + p + 1] - t[k + 1];
+      const double d1 = w[r + p] - w[r], d2 = w[r + p + 1] - w[r + 1];
       if (d1 != 0.0) {  // (u + (t_j - t_k)) / d1 * N_{k,p-1}
-        const double a = (t[j] - t[k]) / d1, b = 1.0 / d1;
+        const double a = (w[kOrder] - w[r]) / d1, b = 1.0 / d1;
+#pragma unroll
         for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r][c] + (c > 0 ? b * P[r][c - 1] : 0.0);
       }
       if (d2 != 0.0 && r < kOrder) {  // ((t_{k+p+1} - t_j) - u) / d2 * N_{k+1,p-1}
-        const double a = (t[k + p + 1] - t[j]) / d2, b = -1.0 / d2;
+        const double a = (w[r + p + 1] - w[kOrder]) / d2, b = -1.0 / d2;
+#pragma unroll
         for (int c = 3; c >= 0; --c) Q[r][c] += a * P[r + 1][c] + (c > 0 ? b * P[r + 1][c - 1] : 0.0);
       }
     }
+#pragma unroll
     for (int r = 0; r <= kOrder; ++r)
+#pragma unroll
       for (int c = 0; c < 4; ++c) P[r][c] = Q[r][c];
   }
+#pragma unroll
   for (int r = 0; r <= kOrder; ++r)  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
+#pragma unroll
     for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
 }
 
-// Whether a knot row is uniform to within rel: h > 0 and every knot within rel * h of
-// t_0 + k h.  Within 1e-3 h the GEMM's direct interval lookup is exact enough; within 1e-5 h
-// the bases are the cardinal cubic pieces to ~1e-5 of a basis value, so the GEMM may
-// evaluate those instead of the table's per-interval cubics (the grids efficient-kan builds,
-// arange * h + a in fp32, are uniform to a few ulps: ~1e-6 h).
-__host__ __device__ inline bool kan_knots_uniform(const float* __restrict__ t, int L, double rel) {
-  if (L < 2) return false;
-  const double h = ((double)t[L - 1] - (double)t[0]) / (L - 1);
-  if (!(h > 0.0) || !(h < 1e300)) return false;
-  for (int k = 0; k < L; ++k)
-    if (!(__builtin_fabs((double)t[k] - ((double)t[0] + k * h)) <= rel * h)) return false;
-  return true;
-}
-constexpr double kUniformRel = 1e-3;   // direct interval lookup
-constexpr double kCardinalRel = 1e-5;  // cardinal pieces in place of the table's cubics
 
 // ---------------------------------------------------------------------------------------
 // Weight preparation, one launch (kan_pack): each output column's scale, the GEMM's weight
@@ -182,24 +249,30 @@ __host__ __device__ constexpr int spline_basis(int s) {
   return kCp == 8 ? (s < 4 ? 2 * s : 2 * (s - 4) + 1) : 4 * (s % 4) + s / 4;
 }
 
-// Basis tables, one thread per table entry (L per feature: the knot row and the L - 1
-// intervals), kThreadsPerBlock entries per workgroup; uflags[block] bit 0: every knot row
-// the block wrote is uniform to 1e-3 h, bit 1: to 1e-5 h (kan_knots_uniform).
-template <int kThreadsPerBlock>
-__device__ __forceinline__ void kan_tables_block(int block, const float* __restrict__ grid, int I, int L,
-                                                 int ngroups, float* __restrict__ tables,
-                                                 int* __restrict__ uflags) {
-  const int idx = block * kThreadsPerBlock + (int)threadIdx.x;
-  const int f = idx / L, j = idx % L - 1;
+// Basis table entries first .. first + count - 1 (L per feature: the knot row and the L - 1
+// intervals), one per thread in turn.  Returns this thread's flags: bit 0 every knot row it
+// wrote is uniform to 1e-3 h, bit 1 to 1e-5 h (kan_knots_uniform); the caller combines them.
+__device__ __forceinline__ int kan_tables_range(int first, int count, const float* __restrict__ grid, int I,
+                                                int L, int ngroups, float* __restrict__ tables) {
   bool uniform = true, cardinal = true;
-  if (f < ngroups * kGroup) {
+  for (int e = (int)threadIdx.x; e < count; e += (int)blockDim.x) {
+    const int idx = first + e;
+    const int f = idx / L, j = idx % L - 1;
+    if (f >= ngroups * kGroup) break;
     float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
                                           (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
     if (f < I) {
-      kan_table_entry(grid + (size_t)f * L, L, j, dst);
+      float kn[kMaxKnots];
+#pragma unroll
+      for (int k = 0; k < kMaxKnots; ++k) kn[k] = k < L ? grid[(size_t)f * L + k] : 0.0f;
+      const bool row_cardinal = kan_knots_uniform(kn, L, kCardinalRel);
+      if (j >= 0 && row_cardinal)
+        kan_cardinal_entry(L, j, kan_row_spacing(kn, L), dst);
+      else
+        kan_table_entry(grid + (size_t)f * L, L, j, dst);
       if (j < 0) {
-        uniform = kan_knots_uniform(grid + (size_t)f * L, L, kUniformRel);
-        cardinal = kan_knots_uniform(grid + (size_t)f * L, L, kCardinalRel);
+        uniform = uniform && kan_knots_uniform(kn, L, kUniformRel);
+        cardinal = cardinal && row_cardinal;
       }
     } else if (j < 0) {  // missing feature: knots 0, 1, 2, ... and zero coefficients
       for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
@@ -207,42 +280,42 @@ __device__ __forceinline__ void kan_tables_block(int block, const float* __restr
       for (int k = 0; k < 16; ++k) dst[kMaxKnots + 16 * j + k] = 0.0f;
     }
   }
-  uniform = __syncthreads_and(uniform);
-  cardinal = __syncthreads_and(cardinal);
-  if (threadIdx.x == 0) uflags[block] = (uniform ? 1 : 0) | (cardinal ? 2 : 0);
+  return (uniform ? 1 : 0) | (cardinal ? 2 : 0);
 }
 
-// kan_pack: the first tblocks workgroups build the basis tables (kan_tables_block); they
-// need nothing from the packing, so they run beside it.  Workgroup tblocks + t owns output
-// columns kPackCols*t .. +kPackCols-1 with kColWaves waves each; wave q of a column takes
-// the runs of 64 features q*64 + 64*kColWaves*j (lane = feature within the run), so a
-// wave's loads cover 64 consecutive features of the column's contiguous rows.  Pass 1
-// reduces the column's max |w| over Wb, sc and Ws to colscale[o] (waves combine through
-// LDS); pass 2 reads the column again (now from the L2 or the Infinity Cache) and writes its
-// hi/lo weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots at
+// kan_pack: the first tblocks workgroups build the basis tables, kPackThreads entries each
+// (kan_tables_range), and write one knot-row flag word each; they need nothing from the
+// packing, so they run beside it.  Workgroup tblocks + t owns output columns kPackCols*t ..
+// +kPackCols-1 with kColWaves waves each (pack_columns); wave q of a column takes the runs
+// of 64 features q*64 + 64*kColWaves*j (lane = feature within the run), so a wave's loads
+// cover 64 consecutive features of the column's contiguous rows.  Pass 1 reduces the
+// column's max |w| over Wb, sc and Ws to colscale[o] (waves combine through LDS); pass 2
+// reads the column again (now from the L2 or the Infinity Cache) and writes its hi/lo
+// weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots at
 // spline_k(f % 32) in the permuted basis order, and lanes with f % 32 < 4 also write silu
-// slots 8 (f % 32) .. +7.  Workgroup tblocks also zeroes kan_fused's
-// split-K arrival counters (their place in the workspace moves with the shape, so every
-// call starts them from zero).
+// slots 8 (f % 32) .. +7.  Workgroup tblocks also zeroes kan_fused's split-K arrival
+// counters (their place in the workspace moves with the shape, so every call starts them
+// from zero).
+// At BASELINE the columns are 512 workgroups, as many as are resident at once, and the 24
+// table workgroups hold slots until they finish, so table time delays the last column
+// workgroups.  Measured (one box, median of 150): 15.6 us without tables, 21.7 us with
+// the recursion indexing whole knot rows, 18.8 us with its 8-knot window, 18.7 us with the
+// closed form for cardinal rows as well; building the tables inside the column workgroups,
+// before or after their columns, measured 23.7-26.7 us.
 constexpr int kPackCols = 2;
 constexpr int kColWaves = 4;
 constexpr int kPackThreads = kPackCols * kColWaves * kWave;
+// Workgroup t's pair of output columns (pass 1 and pass 2 above).
 template <int kCp>
-__global__ __launch_bounds__(kPackThreads) void kan_pack(
-    const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
-    int O, int C, int Opad, float* __restrict__ colscale, _Float16* __restrict__ bhi,
-    _Float16* __restrict__ blo, const float* __restrict__ grid, int L, int ngroups, int tblocks,
-    float* __restrict__ tables, int* __restrict__ uflags, unsigned* __restrict__ counters,
-    int ncounters) {
+__device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb, const float* __restrict__ ws,
+                                             const float* __restrict__ sc, int I, int O, int C, int Opad,
+                                             float* __restrict__ colscale, _Float16* __restrict__ bhi,
+                                             _Float16* __restrict__ blo, int ngroups, unsigned* __restrict__ counters,
+                                             int ncounters) {
   static_assert(kCp % 8 == 0, "whole 8-slot runs");
   __shared__ float colmax[kPackCols][kColWaves];
-  if ((int)blockIdx.x < tblocks) {
-    kan_tables_block<kPackThreads>(blockIdx.x, grid, I, L, ngroups, tables, uflags);
-    return;
-  }
   constexpr int kSub = 1 + kCp;
   constexpr int kStride = kColWaves * kWave;  // features between a wave's runs
-  const int t = (int)blockIdx.x - tblocks;
   if (t == 0)
     for (int i = threadIdx.x; i < ncounters; i += kPackThreads) counters[i] = 0u;
   const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
@@ -387,6 +460,26 @@ __global__ __launch_bounds__(kPackThreads) void kan_pack(
       }
     }
   }
+}
+
+// Four waves per SIMD (at most 128 VGPRs): two workgroups per CU, so 512 column workgroups
+// are resident at once; at 132 VGPRs it was one per CU and twice as slow.
+template <int kCp>
+__global__ __launch_bounds__(kPackThreads) __attribute__((amdgpu_waves_per_eu(4))) void kan_pack(
+    const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
+    int O, int C, int Opad, float* __restrict__ colscale, _Float16* __restrict__ bhi,
+    _Float16* __restrict__ blo, const float* __restrict__ grid, int L, int ngroups, int tblocks,
+    float* __restrict__ tables, int* __restrict__ uflags, unsigned* __restrict__ counters,
+    int ncounters) {
+  const int t = (int)blockIdx.x - tblocks;
+  if (t < 0) {
+    const int b = (int)blockIdx.x;
+    const int flags = kan_tables_range(b * kPackThreads, kPackThreads, grid, I, L, ngroups, tables);
+    const bool uniform = __syncthreads_and(flags & 1), cardinal = __syncthreads_and(flags & 2);
+    if (threadIdx.x == 0) uflags[b] = (uniform ? 1 : 0) | (cardinal ? 2 : 0);
+    return;
+  }
+  pack_columns<kCp>(t, wb, ws, sc, I, O, C, Opad, colscale, bhi, blo, ngroups, counters, ncounters);
 }
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {

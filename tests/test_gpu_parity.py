@@ -103,7 +103,11 @@ def test_baseline_efficient_kan_full(lib):
 # tail; x_range > 1 puts inputs outside the knot span.  Knots: "uniform" (the task's grid:
 # the kernel's direct interval lookup), "random" (sorted random knots: the knot count),
 # "jitter" (uniform plus noise of 1e-4 h: still the direct lookup, which must agree with
-# the exact bases of the jittered knots).
+# the exact bases of the jittered knots), "mixed" (even features the task's grid, odd ones
+# jittered by 1e-4 h: the kernel then reads every row's per-interval cubics, and the even
+# rows' come from the cardinal closed form) and "mixed_edge" (even features jittered by
+# 4e-6 h, still within the 1e-5 h of the closed form, so its cubics meet knots that are
+# not exactly uniform).
 KAN_SHAPES = [
     (130, 45, 70, 5, 3, 1.5, "uniform"),
     (67, 33, 258, 9, 3, 1.0, "random"),
@@ -112,6 +116,8 @@ KAN_SHAPES = [
     (33, 17, 19, 10, 3, 1.0, "uniform"),
     (50, 40, 40, 4, 3, 1.3, "random"),
     (70, 64, 96, 5, 3, 1.2, "jitter"),
+    (70, 64, 96, 5, 3, 1.2, "mixed"),
+    (64, 96, 40, 8, 3, 1.0, "mixed_edge"),
     (21, 40, 50, 6, 2, 1.2, "random"),
     (16, 12, 8, 13, 1, 1.0, "uniform"),
     # Split-K (fewer output tiles than CUs): 64 tiles and 5 feature groups split 2+2+1;
@@ -135,9 +141,13 @@ def test_efficient_kan_shapes(lib, shape):
     L = G + 2 * K + 1
     if knots == "random":
         inp["grid"] = torch.sort(torch.rand(I, L, generator=g) * 3.0 - 1.5, dim=1).values.contiguous()
-    elif knots == "jitter":
+    elif knots in ("jitter", "mixed", "mixed_edge"):
         h = (inp["grid"][0, 1] - inp["grid"][0, 0]).item()
         noise = (torch.rand(I, L, generator=g) * 2 - 1) * 1e-4 * h
+        if knots == "mixed":
+            noise[0::2] = 0.0
+        elif knots == "mixed_edge":
+            noise[0::2] *= 0.04
         inp["grid"] = (inp["grid"] + noise).contiguous()
     want = exact.efficient_kan(inp)["out"]
     for _ in range(2):
