@@ -17,12 +17,14 @@
 // Segments are walked from the row end toward its start with a running carry.  Rows are
 // independent workgroups, so thousands of them stream through the CUs staggered: loads,
 // scans and stores of different rows overlap.  The wave and workgroup scans and the carries
-// between lanes, between waves and between segments are fp64.  A lane's own 4 steps run in
-// fp32: its map's R in pass 1, and in pass 2 the 3 steps after the first, which starts from
-// the fp64 carry.  Within a wave, the carry from one chunk into the chunk before it is the
-// fp32 output at the chunk's first step (widened back to fp64).
-// That adds at most ~2e-7 relative per output (about 1e-6 absolute where terms cancel),
-// against the op's atol = rtol = 1e-5, and measured 1.5-2 % faster than fp64 throughout.
+// between lanes, chunks, waves and segments are fp64.  A lane's own 4 steps run in fp32: its
+// map's R in pass 1, and in pass 2 the 3 steps after the first, which starts from the fp64
+// carry.  That adds at most ~2e-7 relative per output (about 1e-6 absolute where terms
+// cancel), against the op's atol = rtol = 1e-5, and measured 1.5-2 % faster than fp64
+// throughout.  Pass 1 also keeps, for each of a wave's chunks, the composed map of the
+// wave's later chunks (wave-uniform, in scalar registers), so in pass 2 every chunk's
+// incoming value is one fp64 fma of the wave's incoming value and the chunks do not wait on
+// each other; the wave scan's span factors g^(4 * 2^i) are computed once per workgroup.
 // HBM-bound: 9 algorithmic bytes per element (4 reward + 1 done + 4 out).
 #pragma once
 
@@ -32,6 +34,14 @@ namespace taskops {
 
 namespace rtg_detail {
 using f32x4 = float __attribute__((ext_vector_type(4)));
+
+// A wave-uniform double moved to scalar registers (it is the same in every lane).
+__device__ __forceinline__ double uniform(double v) {
+  const long long b = __double_as_longlong(v);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)b);
+  const unsigned hi = (unsigned)__builtin_amdgcn_readfirstlane((int)(unsigned)(b >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
 
 __device__ __forceinline__ double coef(unsigned word, int byte, double g) {
   return ((word >> (8 * byte)) & 0xFFu) ? 0.0 : g;
@@ -74,6 +84,12 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
   double gk = 1.0;
 #pragma unroll
   for (int e = 0; e < kPerLane; ++e) gk *= g;
+  // gpow[i] = g^(kPerLane * 2^i): the wave scan's span factors, the same products as
+  // squaring per step, computed once.
+  double gpow[7];
+  gpow[0] = gk;
+#pragma unroll
+  for (int i = 1; i < 7; ++i) gpow[i] = gpow[i - 1] * gpow[i - 1];
   double pw_rest = 1.0;
   {
     double base = gk;
@@ -137,6 +153,7 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
     double sr[kSeg];
     unsigned long long smask[kSeg];
     double wr = 0.0, wa = 1.0;  // this wave's span map
+    double after_r[kSeg], after_a[kSeg];  // map of this wave's chunks after chunk c
 #pragma unroll
     for (int c = kSeg - 1; c >= 0; --c) {
       float Rf = 0.0f;
@@ -147,17 +164,18 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
 #pragma unroll
       for (int q = 0; q < kQ; ++q) any |= dn[c][q];
       unsigned long long mask = __ballot(any != 0u);
-      double G = gk;  // g^(kPerLane*off)
 #pragma unroll
-      for (int off = 1; off < kWave; off <<= 1) {
+      for (int lv = 0, off = 1; off < kWave; ++lv, off <<= 1) {
         const double Rn = __shfl_down(R, off, kWave);
         const bool blocked = (mask >> lane) & 1ull;
-        if (lane + off < kWave && !blocked) R = fma(G, Rn, R);
+        if (lane + off < kWave && !blocked) R = fma(gpow[lv], Rn, R);
         mask |= mask >> off;
-        G = G * G;
       }
+      const double G = gpow[6];  // g^(kPerLane*64)
       sr[c] = R;
       smask[c] = mask;
+      after_r[c] = uniform(wr);
+      after_a[c] = uniform(wa);
       if (c0 + c < hi) {
         const double cr = __shfl(R, 0, kWave);
         const double ca = (mask & 1ull) ? 0.0 : G;  // G is now g^(kPerLane*64)
@@ -196,18 +214,19 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
       for (int e = 0; e < kPerLane; ++e) asm volatile("" : "+v"(r[c][e]));
 #pragma unroll
       for (int q = 0; q < kQ; ++q) asm volatile("" : "+v"(dn[c][q]));
-      // Value entering this lane's last step: lanes lane+1.. applied to cin.
+      // Value entering this chunk (the wave's later chunks applied to cin), then entering
+      // this lane's last step (lanes lane+1.. applied to it).
+      const double cin_c = fma(after_a[c], cin, after_r[c]);
       const double Rn = __shfl_down(sr[c], 1, kWave);
       const bool later_done = lane + 1 < kWave && ((smask[c] >> (lane + 1)) & 1ull);
       const double An = later_done ? 0.0 : pw_rest;
-      const double vin = (lane == kWave - 1) ? cin : fma(An, cin, Rn);
+      const double vin = (lane == kWave - 1) ? cin_c : fma(An, cin_c, Rn);
       float o[kPerLane];
       // The lane's last step from the fp64 value entering it, the others in fp32.
       o[kPerLane - 1] = (float)fma(coef(dn[c][(kPerLane - 1) / 4], (kPerLane - 1) % 4, g), vin,
                                    (double)r[c][kPerLane - 1]);
 #pragma unroll
       for (int e = kPerLane - 2; e >= 0; --e) o[e] = fmaf(coef32(dn[c][e / 4], e % 4, gf), o[e + 1], r[c][e]);
-      const double v = (double)o[0];
 #pragma unroll
       for (int q = 0; q < kQ; ++q) {
         const int t = t0 + 4 * q;
@@ -225,7 +244,7 @@ __global__ __launch_bounds__(kWaves * 64) void reward_to_go_kernel(
             if (t + e < T) oo[t + e] = o[4 * q + e];
         }
       }
-      cin = __shfl(v, 0, kWave);  // the fp32 output at the chunk's first step
+
     }
     carry = next_carry;
     __syncthreads();  // span_* are rewritten by the next segment
