@@ -14,8 +14,10 @@ SETTLE_MS (the card raises its clock over tens of milliseconds of work: efficien
 measured 452 -> 380 us/call over its first 30 ms), then hipEvents around exactly K
 back-to-back calls on the stream the kernels are launched on, bracketed by device
 synchronisation.  Working sets that fit the 256 MiB Infinity Cache are timed cache-cold
-by rotating input/output copies whose total exceeds it, so the bandwidth figures are HBM
-figures.
+by rotating input/output copies whose total exceeds it, so every call reads its inputs from
+HBM: the bandwidth figures are HBM figures, and efficient_kan's weight preparation reads its
+42 MB of fp32 weights from HBM (2.4 % slower than with one resident copy; fp8_linear is the
+same either way).
 """
 from __future__ import annotations
 
@@ -243,7 +245,7 @@ def main() -> int:
             inp = {k: v for k, v in inp.items() if k not in ("entropy", "entropy_coef")}
         probe = _device_sets(entry, inp, 1)
         per_set = _set_bytes(probe[0])
-        n = _copies(per_set) if bound == "hbm" else 1
+        n = _copies(per_set)
         sets = probe + _device_sets(entry, inp, n - 1)
         call_entry = "ppo_clip_entropy" if key == "ppo_clip" else entry
         _log(f"[bench] {key}: timing {a.steps} calls over {n} rotating copies")
