@@ -274,7 +274,9 @@ def main() -> int:
             roof["call_traffic"] = traffic["call_values"][key]  # every kernel of one call
         r = {"workload": desc, "us_per_call": round(us, 3), "dtype": dtype,
              "algorithmic_" + ("bytes" if bound == "hbm" else "flop"): work,
-             "timing": f"{'cold' if n > 1 else 'resident'}: {n} rotating input copies, {a.steps} calls",
+             "timing": (f"cold: {n} rotating input copies, {a.steps} calls" if n > 1 else
+                        f"cold: one input set of {per_set / 2**20:.0f} MiB, over twice the {MALL_BYTES >> 20} MiB "
+                        f"Infinity Cache, {a.steps} calls"),
              "roofline": roof}
         if not a.no_cpu:
             _log(f"[bench] {key}: CPU eager baseline")
