@@ -203,7 +203,7 @@ def test_gpu_quantize_fallback_path_same_bits(lib, n):
 @pytest.mark.gpu
 def test_gpu_quantize_graph_replay(lib):
     """Captured into a graph, the fused kernel's barrier state carries across replays (the
-    sense flips every launch)."""
+    parity word flips every launch, and each launch clears the other set of words)."""
     n = 300_000
     xd = torch.empty(n, device="cuda")
     q = torch.empty(n, dtype=torch.uint8, device="cuda")
