@@ -40,6 +40,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kGroup = 32;        // features per group
 constexpr int kChunk = 32;        // k per MFMA chunk
@@ -61,7 +62,7 @@ constexpr int BN = 256;
 constexpr int kRB = BM / 16;                        // row blocks per tile (consumer)
 constexpr int kCB = BN / 16 / kConsumerWaves;       // column blocks per consumer wave
 constexpr int kActFragBytes = kRB * 2 * 64 * 16;    // hi + lo activation fragments: 16 KiB
-constexpr int kActIdxBytes = kRB * 64 * 4;          // sparse positions: 2 KiB
+constexpr int kActIdxBytes = kRB * 64 * 4;          // sparse positions, a pair of row blocks per 8 bytes: 2 KiB
 constexpr int kActBytes = kActFragBytes + kActIdxBytes;
 constexpr int kActStages = 2;
 constexpr int kActAt = 0;
@@ -707,7 +708,7 @@ __device__ __forceinline__ void sparse16w(int j, const float (&P)[4], float* v, 
 //     activations and write them to stage (s+1) % 2; wait for the table set and x.
 //
 // LDS (kLdsBytes): 2 activation stages of 18 KiB ([row block][hi, lo][lane] x 16 B, then
-// the positions [row block][lane] x 4 B) and the basis-table window, two sets of 8 (C' = 8)
+// the positions [row block pair][lane][2] x 4 B) and the basis-table window, two sets of 8 (C' = 8)
 // or 4 (C' = 16) feature entries: spline step u's features in set u % 2.
 // ---------------------------------------------------------------------------------------
 
@@ -901,8 +902,10 @@ struct Producer {
       const int frag = 2 * pw + rb;
       *reinterpret_cast<f16x8*>(st + ((frag * 2 + 0) * 64 + lane) * 16) = hi[rb];
       *reinterpret_cast<f16x8*>(st + ((frag * 2 + 1) * 64 + lane) * 16) = lo[rb];
-      if constexpr (kJ > 0) *reinterpret_cast<unsigned*>(st + kActFragBytes + (frag * 64 + lane) * 4) = bits[rb];
     }
+    // Both row blocks' positions side by side: the consumers read a pair's in one 8-byte read.
+    if constexpr (kJ > 0)
+      *reinterpret_cast<i32x2*>(st + kActFragBytes + (pw * 64 + lane) * 8) = i32x2{(int)bits[0], (int)bits[1]};
   }
 
   // Step s = lg * kQ + kJ (the consumers' phases of step s run meanwhile): see the
@@ -982,8 +985,10 @@ __device__ __forceinline__ void read_act(const uint8_t* ast, int lane, int rb, A
     a.h[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(ast + (((rb + r) * 2 + 0) * 64 + lane) * 16));
     if constexpr (kLo)
       a.l[r] = __builtin_bit_cast(f16x8, *reinterpret_cast<const i32x4*>(ast + (((rb + r) * 2 + 1) * 64 + lane) * 16));
-    a.idx[r] = *reinterpret_cast<const int*>(ast + kActFragBytes + ((rb + r) * 64 + lane) * 4);
   }
+  const i32x2 ix = *reinterpret_cast<const i32x2*>(ast + kActFragBytes + ((rb / 2) * 64 + lane) * 8);
+  a.idx[0] = ix.x;
+  a.idx[1] = ix.y;
 }
 
 // Phase L (kH false: hi_a * lo_w) or H (hi_a * hi_w, then lo_a * hi_w) of one step, with the
@@ -1000,7 +1005,7 @@ __device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x
                                               int lane, f32x4 (&acc)[kRB][kCB], Load load, ActPair cur,
                                               ActPair& lfirst, const uint8_t* ast_next = nullptr) {
   constexpr int kTerms = kH ? 2 : 1;
-  constexpr int kReads = kH ? 6 : 4;  // LDS reads of a pair
+  constexpr int kReads = kH ? 5 : 3;  // LDS reads of a pair
   load(0);
   load(1);
   load(2);
@@ -1037,14 +1042,14 @@ __device__ __forceinline__ void consume_phase(const f16x8 (&w0)[kCB], const f16x
       }
     } else if constexpr (kH) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 3; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 2 * kTerms, 0);               // MFMAs
         if (u == 0 || u == 2) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // empty load slot (kept: measured faster)
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < 6; ++u) {
+      for (int u = 0; u < 5; ++u) {
         __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                        // 1 LDS read
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                        // MFMA
         if (u == 0 || u == 3) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // empty load slot (kept: measured faster)
