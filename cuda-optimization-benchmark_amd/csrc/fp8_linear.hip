@@ -3,8 +3,8 @@
 // Drop-in signature tasks/fp8_linear/tests/task.json:3, replacing
 // reference/fp8_linear/solution.cu:276-321.  Kernels are in fp8_linear.hpp: the skinny
 // split-K kernel for M <= 64, the wide (direct-to-LDS, 128-byte rows) kernel when
-// K % 16 == 0 and the operands are 16-byte aligned, and the register-staged tiled kernel
-// otherwise.
+// K % 16 == 0 and the operands are 16-byte aligned (in its 128-row form when 256x256
+// tiles would fill at most half the CUs), and the register-staged tiled kernel otherwise.
 #include "fp8_linear.hpp"
 
 using namespace taskops;
@@ -53,6 +53,21 @@ extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const 
   if (vec == 16) {
     const size_t wide_lds = kWideLdsBytes;
     const uintptr_t o = reinterpret_cast<uintptr_t>(output);
+    if (2 * tiles <= device_cu_count()) {
+      // At most half a 256x256 tile per CU: 128x256 tiles, twice as many workgroups.
+      const dim3 hgrid(((M + kHalfRows - 1) / kHalfRows) * ((N + BN - 1) / BN));
+      const size_t half_lds = kHalfLdsBytes;
+      if (N % 8 == 0 && (o & 15) == 0)
+        hipLaunchKernelGGL(fp8_gemm_half<2>, hgrid, dim3(kThreads), half_lds, stream, x_fp8, w_fp8, (int)M,
+                           (int)N, (int)K, inv, bias, output);
+      else if (N % 4 == 0 && (o & 7) == 0)
+        hipLaunchKernelGGL(fp8_gemm_half<1>, hgrid, dim3(kThreads), half_lds, stream, x_fp8, w_fp8, (int)M,
+                           (int)N, (int)K, inv, bias, output);
+      else
+        hipLaunchKernelGGL(fp8_gemm_half<0>, hgrid, dim3(kThreads), half_lds, stream, x_fp8, w_fp8, (int)M,
+                           (int)N, (int)K, inv, bias, output);
+      return hipGetLastError();
+    }
     if (N % 8 == 0 && (o & 15) == 0)
       hipLaunchKernelGGL(fp8_gemm_wide<2>, dim3(tiles), dim3(kThreads), wide_lds, stream, x_fp8, w_fp8,
                          (int)M, (int)N, (int)K, inv, bias, output);

@@ -15,7 +15,8 @@
 // Three kernels, one launch per call:
 //  * wide (M > 64, K % 16 == 0, 16-byte aligned operands): the main path, described at
 //    fp8_gemm_wide below — direct-to-LDS copies of whole 128-byte row segments into two
-//    64 KiB stages, 32x32x64 MFMAs with fragments read a half-step ahead.
+//    64 KiB stages, 32x32x64 MFMAs with fragments read a half-step ahead.  Grids of at
+//    most half a 256x256 tile per CU take its 128x256-tile form, fp8_gemm_half.
 //  * tiled (M > 64, other K or alignment): 256x256 output tile per workgroup of 4 waves (one per SIMD, each
 //    128x128 = 8x8 MFMA blocks whose 256 fp32 accumulators sit in AGPRs), K in steps of
 //    128 staged through LDS (2 stages x 64 KiB, 16-byte
@@ -265,8 +266,9 @@ __device__ __forceinline__ void wait_vmcnt() {
 // columns go out as one 8-byte store; otherwise one 2-byte store each.  Columns past N
 // get an out-of-range offset and are dropped by the buffer descriptor.  bias_s holds the
 // tile's BN bias values in LDS (zero past N), so no global load sits between the stores.
-template <bool kVec4>
-__device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4], uint16_t* out,
+// kMIx: 32-row x blocks per wave (4 in the 256-row tile, 2 in the 128-row one).
+template <bool kVec4, int kMIx = 4>
+__device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[kMIx][4], uint16_t* out,
                                                        const uint16_t* bias_s, int N, int m0,
                                                        int n0, int wm, int wn, int fr, int fg,
                                                        int rows_a, float inv_scale) {
@@ -281,8 +283,8 @@ __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4]
       const float bv[4] = {__uint_as_float((unsigned)braw.x << 16), __uint_as_float((unsigned)braw.x & 0xffff0000u),
                            __uint_as_float((unsigned)braw.y << 16), __uint_as_float((unsigned)braw.y & 0xffff0000u)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = wm * WM + i * 32 + fr;
+      for (int i = 0; i < kMIx; ++i) {
+        const int row = wm * 32 * kMIx + i * 32 + fr;
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = fmaf(acc[i][j][4 * q + e], inv_scale, bv[e]);
@@ -305,15 +307,16 @@ __device__ __forceinline__ void store_transposed_block(const f32x16 (&acc)[4][4]
   }
 }
 
-// Epilogue through LDS (N % 8 == 0, 16-byte aligned output): the 256x256 bf16 tile is
-// assembled in `tile_s` (128 KiB, the two stages once every copy has landed and every
-// wave is past its last fragment read), then each store instruction writes two whole
+// Epilogue through LDS (N % 8 == 0, 16-byte aligned output): the 256x256 (or 128x256)
+// bf16 tile is assembled in `tile_s` (128 or 64 KiB of the rings, once every copy has
+// landed and every wave is past its last fragment read), then each store instruction writes two whole
 // 512-byte tile rows, instead of 16 bytes into each of 32 rows.  Tile row r's 16-byte
 // chunk c sits at chunk c ^ (r % 32), so both the column-wise writes and the row-wise
 // reads spread over all banks.
 constexpr int kTileRowBytes = BN * 2;  // 512
 constexpr int kCachePolicyNT = 2;       // buffer store cache-policy operand: nt
-__device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16_t* out,
+template <int kMIx = 4>  // 32-row x blocks per wave: the tile has 64 * kMIx rows
+__device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[kMIx][4], uint16_t* out,
                                                const uint16_t* bias_s, uint8_t* tile_s, int N,
                                                int m0, int n0, int wm, int wn, int fr, int fg,
                                                int rows_a, int rows_b, float inv_scale, int tid) {
@@ -326,8 +329,8 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16
       const float bv[4] = {__uint_as_float((unsigned)braw.x << 16), __uint_as_float((unsigned)braw.x & 0xffff0000u),
                            __uint_as_float((unsigned)braw.y << 16), __uint_as_float((unsigned)braw.y & 0xffff0000u)};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = wm * WM + i * 32 + fr;
+      for (int i = 0; i < kMIx; ++i) {
+        const int r = wm * 32 * kMIx + i * 32 + fr;
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = fmaf(acc[i][j][4 * q + e], inv_scale, bv[e]);
@@ -343,8 +346,8 @@ __device__ __forceinline__ void store_tile_lds(const f32x16 (&acc)[4][4], uint16
   const int chunk = lane % 32;
   const bool col_ok = chunk * 8 < rows_b;  // rows_b: valid columns of this tile (N % 8 == 0)
 #pragma unroll 4
-  for (int s = 0; s < BM / 2 / (kThreads / kWave); ++s) {
-    const int r = (wave * (BM / 2 / (kThreads / kWave)) + s) * 2 + lane / 32;
+  for (int s = 0; s < 64 * kMIx / 2 / (kThreads / kWave); ++s) {
+    const int r = (wave * (64 * kMIx / 2 / (kThreads / kWave)) + s) * 2 + lane / 32;
     const i32x4 v = *reinterpret_cast<const i32x4*>(tile_s + r * kTileRowBytes + ((chunk ^ (r & 31)) << 4));
     const unsigned off = (r < rows_a && col_ok) ? (unsigned)(r * N + n0 + chunk * 8) * 2u : kOutOfRange;
     // Non-temporal (streaming) stores: the 32 MB output of a 4096^2 call otherwise sits dirty
@@ -528,6 +531,142 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     store_tile_lds(acc, out, bias_s, smem, N, m0, n0, ewm, ewn, efr, efg, rows_a, rows_b, inv_scale, et);
   else
     store_transposed_block<kStore == 1>(acc, out, bias_s, N, m0, n0, ewm, ewn, efr, efg, rows_a, inv_scale);
+}
+
+// ---------------------------------------------------------------------------------------
+// Half-height wide kernel: 128x256 output tiles (128 x rows, 256 w rows) for grids in
+// which 256x256 tiles would leave half the CUs or more idle (M = 2048, N = 4096 is 128
+// such tiles on 256 CUs).  Same copies, fragment layout, 32x32x64 MFMAs and epilogues as
+// fp8_gemm_wide; the 4 waves are arranged 2 (x) x 2 (w) with 64x128 wave tiles (2 x 4
+// blocks).  A step now moves 16 KiB of x and 32 KiB of w for half the MFMAs, so both
+// operands get a three-slot ring (3 x 16 + 3 x 32 = 144 KiB) and each wave's 12 copies of
+// step kt+2 are spread evenly over the 16 MFMAs of step kt, all into the slots step kt-1
+// left (every wave passed the barrier at step kt-1's mid-step, after its last read of
+// them).  The 12 16-byte fragment reads of each half step (4 w blocks and 2 x blocks, two
+// parts each) ride on its 8 MFMAs, one or two per MFMA.  Accumulation order is the same
+// k-ascending sequence of 64-wide MFMA steps as the 256-row kernel, so the two give the
+// same bits.
+// ---------------------------------------------------------------------------------------
+constexpr int kHalfRows = 128;                                      // x rows per tile
+constexpr int kHalfMI = kHalfRows / 64;                             // 32-row x blocks per wave: 2
+constexpr int kHalfXBytes = kHalfRows * WBK;                        // 16 KiB of x per step
+constexpr int kHalfLdsBytes = 3 * (kHalfXBytes + kWideOperandBytes);  // 144 KiB
+constexpr int kHalfXDma = kHalfRows / 8 / (kThreads / kWave);       // x copies per wave and step: 4
+constexpr int kHalfCopies = kHalfXDma + kWideDmaPerWave;             // 12
+constexpr int kHalfParts = 2 * (4 + kHalfMI);                        // 16-byte reads per half step: 12
+constexpr int kHalfSlots = 4 * kHalfMI;                              // MFMAs per half step: 8
+static_assert(kHalfRows * kTileRowBytes + kBiasBytes <= kHalfLdsBytes, "the output tile and bias fit the rings");
+static_assert(kHalfCopies % 2 == 0, "each half step issues half the copies");
+
+// Group `group` (8 rows) of a tile with 128-byte rows: one direct-to-LDS instruction.
+__device__ __forceinline__ void dma_group128(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows, int K,
+                                             int k0, int group, int lane) {
+  const int row = group * 8 + lane / 8;
+  const int gk = k0 + 16 * ((lane % 8) ^ swz128(row));
+  const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off, 0, 0, 0);
+}
+
+template <int kStore>
+__global__ __launch_bounds__(kThreads) void fp8_gemm_half(
+    const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
+    float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const int tm = (M + kHalfRows - 1) / kHalfRows, tn = (N + BN - 1) / BN;
+  int mt, nt;
+  tile_of(blockIdx.x, tm, tn, mt, nt);
+  const int m0 = mt * kHalfRows, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int rows_a = min(kHalfRows, M - m0), rows_b = min(BN, N - n0);
+  const __amdgpu_buffer_rsrc_t xa = make_rsrc(x + (size_t)m0 * K, (size_t)rows_a * K);
+  const __amdgpu_buffer_rsrc_t wb = make_rsrc(w + (size_t)n0 * K, (size_t)rows_b * K);
+
+  f32x16 acc[kHalfMI][4];
+#pragma unroll
+  for (int i = 0; i < kHalfMI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x16{};
+
+  const int nk = (K + WBK - 1) / WBK;
+  // As in fp8_gemm_wide, copies past the last step zero-fill a free slot.
+  auto a_tile = [&](int step) { return smem + (step % 3) * kHalfXBytes; };
+  auto b_tile = [&](int step) { return smem + 3 * kHalfXBytes + (step % 3) * kWideOperandBytes; };
+  // Copy c (0 .. 11) of this wave for `step`: x groups first, then w groups.
+  auto copy = [&](int step, int c) {
+    if (c < kHalfXDma)
+      dma_group128(xa, a_tile(step), rows_a, K, step * WBK, wave * kHalfXDma + c, lane);
+    else
+      dma_group128(wb, b_tile(step), rows_b, K, step * WBK, wave * kWideDmaPerWave + c - kHalfXDma, lane);
+  };
+  const int fr = lane % 32, fg = lane / 32;
+  const int arow = wm * 32 * kHalfMI + fr, brow = wn * WN + fr;
+  // 16-byte part p of `half` of step `step`: parts 0..7 are w blocks 0..3, 8..11 x blocks.
+  auto part_of = [&](int step, int p, int half) {
+    return p < 8 ? frag128_part(b_tile(step), brow + 32 * (p / 2), fg, half, p % 2)
+                 : frag128_part(a_tile(step), arow + 32 * ((p - 8) / 2), fg, half, p % 2);
+  };
+
+  // Prologue: steps 0 and 1, then step 0's first-half fragments.
+#pragma unroll
+  for (int c = 0; c < kHalfCopies; ++c) copy(0, c);
+#pragma unroll
+  for (int c = 0; c < kHalfCopies; ++c) copy(1, c);
+  wait_vmcnt<kHalfCopies>();
+  __syncthreads();
+  i32x8 a0[kHalfMI], b0[4], a1[kHalfMI], b1[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) b0[j] = frag128(b_tile(0), brow + 32 * j, fg, 0);
+#pragma unroll
+  for (int i = 0; i < kHalfMI; ++i) a0[i] = frag128(a_tile(0), arow + 32 * i, fg, 0);
+
+  // One half step: the MFMAs on (a, b), copies c0 .. c0+5 of step kt+2 and the parts of
+  // `half` of step `rstep` into (na, nb).
+  auto half_step = [&](const i32x8 (&a)[kHalfMI], const i32x8 (&b)[4], i32x8 (&na)[kHalfMI], i32x8 (&nb)[4],
+                       int kt, int c0, int rstep, int half) {
+    i32x4 part[kHalfParts];
+#pragma unroll
+    for (int s = 0; s < kHalfSlots; ++s) {
+      const int i = s / 4, j = s % 4;
+      acc[i][j] = mfma32_e4m3(b[j], a[i], acc[i][j]);
+#pragma unroll
+      for (int c = (kHalfCopies / 2) * s / kHalfSlots; c < (kHalfCopies / 2) * (s + 1) / kHalfSlots; ++c)
+        copy(kt + 2, c0 + c);
+#pragma unroll
+      for (int p = kHalfParts * s / kHalfSlots; p < kHalfParts * (s + 1) / kHalfSlots; ++p)
+        part[p] = part_of(rstep, p, half);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) nb[j] = join(part[2 * j], part[2 * j + 1]);
+#pragma unroll
+    for (int i = 0; i < kHalfMI; ++i) na[i] = join(part[8 + 2 * i], part[9 + 2 * i]);
+  };
+
+  for (int kt = 0; kt < nk; ++kt) {
+    // First half: MFMAs on step kt's first 64 k, reading its second 64 k.
+    half_step(a0, b0, a1, b1, kt, 0, kt, 1);
+    // Step kt+1 landed (only step kt+2's first six copies may be outstanding), and every
+    // wave holds step kt in registers.
+    wait_vmcnt<kHalfCopies / 2>();
+    barrier_no_vm_drain();
+    // Second half: MFMAs on step kt's second 64 k, reading step kt+1's first 64 k.
+    half_step(a1, b1, a0, b0, kt, kHalfCopies / 2, kt + 1, 0);
+  }
+  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
+  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + kHalfRows * kTileRowBytes);
+  bias_s[tid] = bias_v;
+  __syncthreads();
+  int et = tid;
+  asm volatile("" : "+v"(et));
+  const int ew = et / kWave, el = et % kWave;
+  const int ewm = ew / kWavesN, ewn = ew % kWavesN, efr = el % 32, efg = el / 32;
+  if constexpr (kStore == 2)
+    store_tile_lds<kHalfMI>(acc, out, bias_s, smem, N, m0, n0, ewm, ewn, efr, efg, rows_a, rows_b, inv_scale, et);
+  else
+    store_transposed_block<kStore == 1, kHalfMI>(acc, out, bias_s, N, m0, n0, ewm, ewn, efr, efg, rows_a, inv_scale);
 }
 
 // ---------------------------------------------------------------------------------------

@@ -159,9 +159,16 @@ def test_efficient_kan_shapes(lib, shape):
 # (M, K, N, output offset in bf16 elements).  K % 16 == 0 with 16-byte aligned operands
 # runs the wide kernel: its three epilogues (N % 8 == 0 and a 16-byte aligned output; N % 4
 # == 0 and 8-byte aligned; otherwise), M and N tile tails, K not a multiple of its 128-wide
-# step.  K % 16 != 0 runs the tiled kernel; M <= 64 the skinny (flat loads through LDS when
-# K % 16 == 0, loads in the MFMA layout otherwise).
+# step.  Up to 128 tiles of 256x256 (half the 256 CUs) it runs in its 128x256-tile form
+# (fp8_gemm_half): every wide shape below up to the reference's timed M=2048 K=1024 N=4096;
+# the M=2200 shapes (9 x 16 tiles) run the 256x256 form with the same tails.  K % 16 != 0
+# runs the tiled kernel; M <= 64 the skinny (flat loads through LDS when K % 16 == 0, loads
+# in the MFMA layout otherwise).
 FP8_SHAPES = [
+    (2048, 1024, 4096, 0),
+    (2200, 144, 4000, 0),
+    (2200, 144, 4004, 4),
+    (2200, 176, 3999, 0),
     (300, 192, 264, 0),
     (300, 192, 264, 4),
     (257, 48, 260, 0),
