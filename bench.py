@@ -65,13 +65,25 @@ WORKLOADS = {
                    "fp8_linear M=4096 K=N=4096 e4m3 -> bf16"),
     "fp8_linear_m16": ("fp8_linear", "fp8_linear_m16", "hbm", 16_982_016, "fp8",
                        "fp8_linear M=16 K=N=4096 e4m3 -> bf16 (weight stream)"),
+    # Not a BASELINE.json config: the reference's own timed fp8_linear case (its harness
+    # times this shape), with that case's input distributions.
+    "fp8_linear_timed": ("fp8_linear", "timed:fp8_linear", "mfma", 17_179_869_184, "fp8",
+                         "fp8_linear M=2048 K=1024 N=4096 e4m3 -> bf16 (the reference's timed case)"),
     # Not a task op: the per-tensor quantiser that makes fp8_linear's operands, run over the
     # BASELINE x (4096x4096 bf16-rounded N(0,1), fp32).  4 bytes in + 1 out per element.
     "quantize_e4m3": ("quantize_e4m3", "fp8_linear", "hbm", 5 * 4096 * 4096, "f32",
                       "quantize_e4m3 x fp32 [4096,4096] -> e4m3 + fp32 scale (fp8_linear operand)"),
 }
 ORDER = ["reward_to_go", "pow_abs_sqrt_mean", "leaky", "ppo_clip", "ppo_clip_dropin", "efficient_kan",
-         "fp8_linear", "fp8_linear_m16", "quantize_e4m3"]
+         "fp8_linear", "fp8_linear_m16", "fp8_linear_timed", "quantize_e4m3"]
+
+
+def _case(bkey: str) -> dict:
+    """The input case of a workload: a BASELINE key, or "timed:<op>" for the op's timed case."""
+    from cob_amd import tasks
+    if bkey.startswith("timed:"):
+        return tasks.timed_case(bkey.split(":", 1)[1])
+    return tasks.BASELINE[bkey]
 
 
 def _log(msg: str) -> None:
@@ -238,7 +250,7 @@ def main() -> int:
     results = {}
     for key in ops:
         entry, bkey, bound, work, dtype, desc = WORKLOADS[key]
-        case = tasks.BASELINE[bkey]
+        case = _case(bkey)
         _log(f"[bench] {key}: generating inputs")
         inp = _quant_inputs(case) if entry == "quantize_e4m3" else inputs.make_inputs(entry, case)
         if key == "ppo_clip_dropin":

@@ -45,6 +45,7 @@ DOMINANT = {
     "efficient_kan": "kan_fused",
     "fp8_linear": "fp8_gemm_wide",
     "fp8_linear_m16": "fp8_gemm_skinny_flat",
+    "fp8_linear_timed": "fp8_gemm_half",
     "quantize_e4m3": "qz_fused",
 }
 # Every kernel one call launches, for the ops that launch more than one; their traffic is

@@ -164,6 +164,11 @@ def load_task(op: str) -> dict:
     return t
 
 
+def timed_case(op: str) -> dict:
+    """The case the reference's harness times for `op` (one per task)."""
+    return copy.deepcopy(next(c for c in _HIDDEN[op] if c["timed"]))
+
+
 def all_cases(op: str) -> list[dict]:
     """Hidden then public cases (public names get a `public_` prefix)."""
     out = copy.deepcopy(_HIDDEN[op])
