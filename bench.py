@@ -294,7 +294,7 @@ def main() -> int:
             _log(f"[bench] {key}: CPU eager baseline")
             sec, reps = time_cpu(entry, inp)
             r["cpu_baseline"] = {"value": round(sec * 1e6, 1), "unit": "us/call", "cores": cores, "kind": "port",
-                                 "sample": f"full BASELINE workload, median of {max(1, reps - 1)} warm run(s) "
+                                 "sample": f"the full workload above, median of {max(1, reps - 1)} warm run(s) "
                                            f"of oracle/eager.py (fp32 torch CPU, {cores} threads)"}
             r["speedup_vs_cpu"] = round(sec * 1e6 / us, 1)
         results[key] = r
