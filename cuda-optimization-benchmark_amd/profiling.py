@@ -205,6 +205,10 @@ def main(argv=None) -> int:
     m.add_argument("--simds", type=int, default=MI355X_SIMDS)
     m.add_argument("--xcds", type=int, default=MI355X_XCDS)
     m.add_argument("--json", help="write {bench op key: MFMA busy %% of its dominant kernel}")
+    c = sub.add_parser("counters", help="mean of each named counter per dispatch, for kernels matching --kernel")
+    c.add_argument("dir")
+    c.add_argument("names", nargs="+")
+    c.add_argument("--kernel", default="", help="substring of the kernel names to show")
     t = sub.add_parser("traffic")
     t.add_argument("fetch_dir")
     t.add_argument("write_dir")
@@ -215,6 +219,13 @@ def main(argv=None) -> int:
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print_stats(a.dir)
+    elif a.cmd == "counters":
+        print("| counter | kernel | dispatches | mean per dispatch |")
+        print("|---|---|---:|---:|")
+        for name in a.names:
+            for k, vs in sorted(counter_values(a.dir, name).items()):
+                if a.kernel in k and vs:
+                    print(f"| {name} | `{_short(k, 48)}` | {len(vs)} | {statistics.mean(vs):.4g} |")
     elif a.cmd == "mfma":
         u = mfma_util(a.dir, a.simds, a.xcds)
         print_mfma(u)

@@ -126,3 +126,20 @@ def test_profiling_json_writer(tmp_path):
     out = tmp_path / "x.json"
     profiling._write_json(str(out), {"values": {"leaky": 1}}, SimpleNamespace(source="profiles/a.md", commit="abc1234"))
     assert json.loads(out.read_text()) == {"values": {"leaky": 1}, "source": "profiles/a.md", "commit": "abc1234"}
+
+
+def test_profiling_counters_table(tmp_path, capsys):
+    """profiling.py counters: per kernel, the mean over dispatches of a counter summed over
+    its instances, for the kernels whose names contain --kernel."""
+    import sqlite3
+    from cob_amd import profiling
+    db = sqlite3.connect(tmp_path / "p_results.db")
+    db.execute("create table counters_collection (kernel_name text, dispatch_id int, counter_name text, value real)")
+    rows = [("fp8_gemm_half<2>", 1, "SQ_X", 3.0), ("fp8_gemm_half<2>", 1, "SQ_X", 5.0),
+            ("fp8_gemm_half<2>", 2, "SQ_X", 10.0), ("other", 3, "SQ_X", 99.0), ("fp8_gemm_half<2>", 1, "SQ_Y", 7.0)]
+    db.executemany("insert into counters_collection values (?, ?, ?, ?)", rows)
+    db.commit()
+    db.close()
+    assert profiling.main(["counters", str(tmp_path), "SQ_X", "--kernel", "fp8_gemm"]) == 0
+    lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("| SQ_")]
+    assert lines == ["| SQ_X | `fp8_gemm_half<2>` | 2 | 9 |"]
