@@ -517,7 +517,11 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
   // The bias (L2-resident) is loaded only now: no LDS is free during the loop and a
   // register held through it would spill.
   const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
-  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
+  // bias_s lies in w slot 1, where the zero-filling copies of step nk+1 land when nk is
+  // even, and each wave's vmcnt covers only its own copies: every wave drains its copies
+  // and passes a barrier before any wave writes the bias there.
+  wait_vmcnt<0>();
+  __syncthreads();
   uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + BM * kTileRowBytes);
   bias_s[tid] = bias_v;
   __syncthreads();
@@ -655,7 +659,11 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
     half_step(a1, b1, a0, b0, kt, kHalfCopies / 2, kt + 1, 0);
   }
   const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
-  wait_vmcnt<0>();  // no copy may still be writing LDS when the workgroup exits
+  // bias_s lies in w ring slot 0, where the zero-filling copies of step nk+1 land when
+  // nk % 3 == 2 (K = 1024), and each wave's vmcnt covers only its own copies: every wave
+  // drains its copies and passes a barrier before any wave writes the bias there.
+  wait_vmcnt<0>();
+  __syncthreads();
   uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + kHalfRows * kTileRowBytes);
   bias_s[tid] = bias_v;
   __syncthreads();

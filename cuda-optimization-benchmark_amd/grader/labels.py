@@ -3,22 +3,34 @@
 The label vocabulary is the reference's (graders/verdict.py:35-61), because its users read
 these words: timeout, cuda error, out-of-bounds write, input modified, crash, wrong shape,
 unwritten output, wrong value, stale state; a kernel that passes some passes and fails
-others is a flip.  Here each label is one rule over the case report of
-grader/protocol.py, and the rules are tried in the order of RULES: the first that finds
-something names the failure and where it was seen.
+others is a flip.  The report is read in stages (STAGES), as the reference reads its case
+record: the process state, then each call in call order with that call's own checks in the
+order cuda error, out-of-bounds write, input modified, then the process state again, then
+each output of judged call 1 (wrong shape, unwritten output, wrong value) and each output
+of judged call 2 (stale state).  The first check that finds something names the failure
+and where it was seen, so an input changed on call 1 outranks a guard hit on call 2.
 """
 from __future__ import annotations
 
 
-def _per_call(test):
-    """A rule that applies `test(call record) -> str | None` to each call in turn."""
-    def rule(report):
+def _state(label, *states):
+    """A stage that fires when the report's process state is one of `states`."""
+    def stage(report):
+        return (label, report.get("state")) if report.get("state") in states else None
+    return stage
+
+
+def _each_call(*checks):
+    """A stage that walks the calls in order and tries each call's `(label, test(call
+    record) -> str | None)` checks in turn."""
+    def stage(report):
         for c in report.get("calls", []):
-            found = test(c)
-            if found:
-                return f"call {c['call']}: {found}"
+            for label, test in checks:
+                found = test(c)
+                if found:
+                    return label, f"call {c['call']}: {found}"
         return None
-    return rule
+    return stage
 
 
 def _stray_in(prefix):
@@ -28,31 +40,33 @@ def _stray_in(prefix):
     return test
 
 
-def _judged(call, test):
-    """A rule over the tallies of one judged call."""
-    def rule(report):
+def _each_output(call, *checks):
+    """A stage over the tallies of one judged call: for each output that disagrees, in
+    output order, the first `(label, test(tally))` that holds names it."""
+    def stage(report):
         for name, t in (report.get("checks") or {}).get(str(call), {}).items():
-            if test(t):
-                return f"call {call}: {name}"
+            if t["mismatched"] > 0 or not t["size_ok"]:
+                label = next((lab for lab, test in checks if test(t)), checks[-1][0])
+                return label, f"call {call}: {name}"
         return None
-    return rule
+    return stage
 
 
-def _state(*states):
-    return lambda report: report.get("state") if report.get("state") in states else None
-
-
-RULES = (
-    ("timeout", _state("timeout")),
-    ("cuda error", _per_call(lambda c: c.get("error"))),
-    ("out-of-bounds write", _per_call(_stray_in("gap"))),
-    ("input modified", _per_call(_stray_in("input"))),
-    ("crash", _state("crashed")),
-    ("wrong shape", _judged(1, lambda t: not t["size_ok"])),
-    ("unwritten output", _judged(1, lambda t: t["mismatched"] > 0 and t["unwritten"] == t["mismatched"])),
-    ("wrong value", _judged(1, lambda t: t["mismatched"] > 0)),
-    ("stale state", _judged(2, lambda t: t["mismatched"] > 0)),
+STAGES = (
+    _state("timeout", "timeout"),
+    _each_call(("cuda error", lambda c: c.get("error")),
+               ("out-of-bounds write", _stray_in("gap")),
+               ("input modified", _stray_in("input"))),
+    _state("crash", "crashed"),
+    _each_output(1, ("wrong shape", lambda t: not t["size_ok"]),
+                 ("unwritten output", lambda t: t["unwritten"] == t["mismatched"]),
+                 ("wrong value", lambda t: True)),
+    _each_output(2, ("stale state", lambda t: True)),
 )
+
+# Every label a stage can give, in the order a single call's (or output's) checks try them.
+LABELS = ("timeout", "cuda error", "out-of-bounds write", "input modified", "crash", "wrong shape",
+          "unwritten output", "wrong value", "stale state")
 
 
 def case_outcome(report: dict) -> dict:
@@ -61,9 +75,10 @@ def case_outcome(report: dict) -> dict:
     kernel was seen)."""
     if report.get("state") == "not started" or (report.get("state") != "timeout" and not report.get("calls")):
         return {"outcome": "grader_error", "label": None, "where": "before call 1"}
-    for label, rule in RULES:
-        where = rule(report)
-        if where:
+    for stage in STAGES:
+        found = stage(report)
+        if found:
+            label, where = found
             return {"outcome": "timeout" if label == "timeout" else "fail", "label": label, "where": where}
     return {"outcome": "pass", "label": None, "where": None}
 

@@ -13,7 +13,7 @@ from cob_amd import tasks
 from cob_amd.grader import signature
 from cob_amd.grader.arena import ALIGN, GUARD_BYTES, GUARD_FILL, POISON_FILL, Arena
 from cob_amd.grader.entry import pack
-from cob_amd.grader.labels import RULES, case_outcome, kernel_status
+from cob_amd.grader.labels import LABELS, case_outcome, kernel_status
 from cob_amd.grader.tolerance import tally
 
 
@@ -220,13 +220,24 @@ def test_case_labels(report, outcome, label, where):
 
 
 def test_label_precedence():
-    """When several things are wrong at once the earlier rule names the failure."""
-    order = [label for label, _ in RULES]
-    assert order.index("out-of-bounds write") < order.index("input modified") < order.index("wrong value")
+    """Calls are read one at a time, each with its checks in the order cuda error,
+    out-of-bounds write, input modified, as graders/verdict.py:37-44 reads them: a change
+    to an input on call 1 outranks a guard hit on call 2, and within one call the guard hit
+    comes first.  Judged outputs are read one at a time, in output order."""
+    assert LABELS.index("out-of-bounds write") < LABELS.index("input modified") < LABELS.index("wrong value")
     r = _report(calls__0__strays=INP, calls__1__strays=GAP, checks__1__out__mismatched=1)
+    assert (case_outcome(r)["label"], case_outcome(r)["where"]) == ("input modified", "call 1: input x (byte 4096, 2 bytes)")
+    r = _report(calls__1__strays=INP + GAP)
+    assert case_outcome(r)["label"] == "out-of-bounds write"
+    r = _report(calls__2__error="launch failure", calls__0__strays=GAP)
     assert case_outcome(r)["label"] == "out-of-bounds write"
     r = _report(checks__1__out__mismatched=1, checks__2__out__mismatched=1)
     assert case_outcome(r)["label"] == "wrong value"
+    r = _report(checks__1__out__mismatched=2)
+    r["checks"]["1"]["other"] = dict(r["checks"]["1"]["out"], size_ok=False, mismatched=10)
+    assert (case_outcome(r)["label"], case_outcome(r)["where"]) == ("wrong value", "call 1: out")
+    r["checks"]["1"]["out"]["mismatched"] = 0
+    assert (case_outcome(r)["label"], case_outcome(r)["where"]) == ("wrong shape", "call 1: other")
 
 
 def test_kernel_status_over_passes():
