@@ -63,7 +63,7 @@ MALL_BYTES = 256 << 20
 
 # op key -> (entry op, BASELINE key, bound, algorithmic work per call, dtype, description)
 WORKLOADS = {
-    "reward_to_go": ("reward_to_go", "reward_to_go", "hbm", 150_994_944, "f32 lane steps, f64 scans/carries",
+    "reward_to_go": ("reward_to_go", "reward_to_go", "hbm", 150_994_944, "f32 lane steps and wave scans, f64 carries",
                      "reward_to_go B=4096 T=4096 gamma=0.99 done_p=0.01 (BASELINE configs[1])"),
     "pow_abs_sqrt_mean": ("pow_abs_sqrt_mean", "pow_abs_sqrt_mean", "hbm", 536_870_916, "f32",
                           "pow_abs_sqrt_mean inp,target fp32 [16,4,1024,1024] N(0,1)"),

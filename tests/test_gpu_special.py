@@ -79,6 +79,21 @@ def test_rtg_gamma_one_suffix_sums(lib):
     _agree("reward_to_go", got.numpy(), suffix)
 
 
+def test_rtg_gamma_one_signed_rewards_full_rows(lib):
+    """gamma = 1, U[-1, 1] rewards, no done step, BASELINE row length: the case where the
+    fp32 lane steps' and wave scan's rounding errors never decay along the row, and outputs
+    cross zero (where the bound is atol alone).  The task's rule must hold everywhere."""
+    print("\n[special] reward_to_go gamma 1, U[-1,1], no done, T=4096", flush=True)
+    g = torch.Generator().manual_seed(4410)
+    B, T = 256, 4096
+    inp = {"reward": torch.rand(B, T, generator=g) * 2 - 1, "done": torch.zeros(B, T, dtype=torch.bool),
+           "gamma": 1.0, "B": B, "T": T}
+    got = capi.run_op(lib, "reward_to_go", inp)["output"].cpu()
+    t = tally(got, exact.reward_to_go(inp)["output"], tasks.load_task("reward_to_go")["tolerance"])
+    print(f"[special] worst error {t['worst']:.4f} of the tolerance", flush=True)
+    assert t["mismatched"] == 0, t
+
+
 # ---- ppo_clip -----------------------------------------------------------------------------
 
 @pytest.mark.parametrize("n", [(7, 13, 3), (4096, 256, 1)])
