@@ -107,6 +107,13 @@ hipError_t taskops_ppo_clip_entropy_noalloc(int32_t B, int32_t T, int32_t H,
  *                              + bsplines(x; grid) @ (spline_weight * spline_scaler[...,None])^T
  * grid is [I, grid_size + 2*spline_order + 1] (per-feature knots, strictly increasing),
  * spline_weight is [O, I, grid_size + spline_order].  fp32 in and out.
+ * Spline order 3 with at most 16 knots per feature takes the fp16x3 MFMA path, whose limits
+ * are: |x| < 65504 (silu(x) is carried in fp16 halves); within one output column the
+ * nonzero entries of base_weight and spline_weight*spline_scaler span at most about 2^24
+ * in magnitude (smaller ones lose bits to the fp16 low halves); knot rows uniform to
+ * 5e-7 h use the cardinal cubic pieces (about 1e-6 of a basis value from the exact bases),
+ * all other rows exact per-interval cubics.  Other orders and knot counts take an fp32
+ * row-wise path without these limits.
  * Replaces: reference/efficient_kan/solution.cu:177-288
  *           (tasks/efficient_kan/tests/task.json:3; op: reference.py:33-51). */
 hipError_t taskops_efficient_kan(const float* x, const float* grid, const float* base_weight,

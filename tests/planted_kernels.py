@@ -138,8 +138,9 @@ class DeviceFault:
 
 
 class PlantedLibrary:
-    """A GPU runner: lib/planted_<op>.so with `fault` selected.  One runner grades one case
-    (the library counts its calls from the selection, for the cached and call-3 kinds)."""
+    """A GPU runner: lib/planted_<op>.so with `fault` selected.  The library counts its
+    calls from the selection (for the cached and call-3 kinds), so a runner that grades
+    several cases is restarted by start_case() before each."""
 
     def __init__(self, op: str, fault: str | None = None):
         import ctypes
@@ -148,10 +149,16 @@ class PlantedLibrary:
         from cob_amd.grader.plants import KINDS
         path = LIB_DIR / f"planted_{op}.so"
         self.lib = DropInLibrary(op, path=path)
-        select = ctypes.CDLL(str(path)).planted_select
-        select.argtypes = [ctypes.c_int]
-        select.restype = None
-        select(KINDS.index(fault or "none"))
+        self._select = ctypes.CDLL(str(path)).planted_select
+        self._select.argtypes = [ctypes.c_int]
+        self._select.restype = None
+        self._kind = KINDS.index(fault or "none")
+        self._select(self._kind)
+
+    def start_case(self):
+        """Select the kind again, which restarts the library's call count: each graded case
+        then sees calls 1, 2, 3 (the reference grades each case in its own process)."""
+        self._select(self._kind)
 
     def bind(self, arena, scalars):
         return self.lib.bind(arena, scalars)

@@ -92,15 +92,22 @@ def test_cli(tmp_path, capsys):
 @pytest.mark.gpu
 @pytest.mark.timeout(400)
 def test_grade_driver_on_gpu(tmp_path):
-    """tests/grade_gpu.py end to end on two ops: logs, verdict rows and the table."""
+    """tests/grade_gpu.py end to end on two ops: logs, verdict rows, the table and the
+    proof record, the planted libraries graded after the drop-ins."""
     import subprocess
     import sys
     from pathlib import Path
+    from cob_amd.grader.plants import KINDS
     print("\n[grade] reward_to_go, fp8_linear", flush=True)
     drv = Path(__file__).resolve().parent / "grade_gpu.py"
     r = subprocess.run([sys.executable, "-u", str(drv), str(tmp_path), "--ops", "reward_to_go,fp8_linear",
                         "--passes", "1"], capture_output=True, text=True, timeout=360)
     assert r.returncode == 0, (r.stdout[-2000:], r.stderr[-3000:])
     rows = json.loads((tmp_path / "verdicts.json").read_text())
-    assert {r["task"]: r["status"] for r in rows.values()} == {"reward_to_go": "pass", "fp8_linear": "pass"}
-    assert all(r["kernel_ms"] > 0 and r["x_eager"] > 1 and r["launches_per_call"] == 1 for r in rows.values())
+    dropins = {k: v for k, v in rows.items() if k.startswith("taskops_")}
+    assert {r["task"]: r["status"] for r in dropins.values()} == {"reward_to_go": "pass", "fp8_linear": "pass"}
+    assert all(r["kernel_ms"] > 0 and r["x_eager"] > 1 and r["launches_per_call"] == 1 for r in dropins.values())
+    assert len(rows) == 2 + 2 * len(KINDS)
+    proof = json.loads((tmp_path / "proof.json").read_text())
+    assert proof["summary"] == {"references_pass": 2, "references": 2,
+                                "planted_as_expected": 2 * len(KINDS), "planted": 2 * len(KINDS)}, proof["planted"]
