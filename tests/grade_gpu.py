@@ -100,9 +100,10 @@ def proof_table(res: dict) -> str:
     lines = [f"references_pass {s['references_pass']}/{s['references']}, "
              f"planted_as_expected {s['planted_as_expected']}/{s['planted']}", "",
              "| drop-in | status | label | identical repeat | kernel ms | x eager |", "|---|---|---|---|---:|---:|"]
+    num = lambda x: "" if x is None else f"{x:.4g}"
     for op, v in res["references"].items():
         lines.append(f"| {op} | {v['status']} | {v['label'] or ''} | {v['repeat_identical']} | "
-                     f"{v['kernel_ms'] if v['kernel_ms'] is not None else ''} | {v['x_eager'] if v['x_eager'] is not None else ''} |")
+                     f"{num(v['kernel_ms'])} | {num(v['x_eager'])} |")
     lines += ["", "| planted library / kind | expected | status | label | identical repeat | as expected |",
               "|---|---|---|---|---|---|"]
     for name, v in res["planted"].items():
