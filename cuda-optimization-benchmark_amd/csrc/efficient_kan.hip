@@ -109,8 +109,10 @@ hipError_t launch_fast(const float* x, const float* grid, const float* wb, const
   auto* partial = reinterpret_cast<float*>(static_cast<char*>(wsp) + partial_at);
   // One launch finds the column scales, packs the weights and builds the basis tables and
   // their uniform-grid flags.
-  hipLaunchKernelGGL(kan_pack<kCp>, dim3(Opad / kPackCols + table_blocks), dim3(kPackThreads), 0, stream, wb, ws, sc,
-                     I, O, C, Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags, counters,
+  const bool vecw = C % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
+  auto pack = vecw ? kan_pack<kCp, true> : kan_pack<kCp, false>;
+  hipLaunchKernelGGL(pack, dim3(Opad / kPackCols + table_blocks), dim3(kPackThreads), 0, stream, wb, ws, sc, I, O, C,
+                     Opad, colscale, bhi, blo, grid, L, ngroups, table_blocks, tables, uflags, counters,
                      nsplit > 1 ? tiles : 0);
   e = hipGetLastError();
   if (e != hipSuccess) return e;

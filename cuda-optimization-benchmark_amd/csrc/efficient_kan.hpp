@@ -313,7 +313,7 @@ constexpr int kPackCols = 2;
 constexpr int kColWaves = 4;
 constexpr int kPackThreads = kPackCols * kColWaves * kWave;
 // Workgroup t's pair of output columns (pass 1 and pass 2 above).
-template <int kCp>
+template <int kCp, bool kVecW>
 __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb, const float* __restrict__ ws,
                                              const float* __restrict__ sc, int I, int O, int C, int Opad,
                                              float* __restrict__ colscale, _Float16* __restrict__ bhi,
@@ -330,12 +330,12 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
   const int o = t * kPackCols + oc;
   const int first = q * kWave + lane;
   const bool col = o < O;
-  const bool vec = C % 4 == 0 && (reinterpret_cast<uintptr_t>(ws) & 15) == 0;
+  constexpr bool vec = kVecW;  // C % 4 == 0 and ws 16-byte aligned: 16-byte row loads
   const float* wsc = ws + (size_t)o * I * C;
   // Ws[o, f, c] for c < kCp (zero past C), times s.
   auto spline_row = [&](int f, float s, float (&v)[kCp]) {
     const float* row = wsc + (size_t)f * C;
-    if (vec) {
+    if constexpr (vec) {
 #pragma unroll
       for (int c4 = 0; c4 < kCp / 4; ++c4) {
         f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
@@ -350,39 +350,55 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
   };
 
   // Pass 1: max over the column.  max_c |ws * s| = |s| * max_c |ws| exactly (rounding is
-  // monotonic); a wave's runs go four at a time so each lane keeps its loads in flight.  The
-  // last four runs stay in registers for pass 2.
+  // monotonic).  A wave's runs go four at a time, and every load of a batch is a buffer
+  // load with no branch around it (an offset past the buffer reads zero for a missing
+  // feature, column or basis), so all of them are in flight before the first is used:
+  // behind per-run branches the compiler waited for each run's loads before issuing the
+  // next run's, one memory round trip per run.  The last four runs stay in registers for
+  // pass 2.
+  const __amdgpu_buffer_rsrc_t rwb = make_rsrc(wb, (size_t)O * I * 4);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc, (size_t)O * I * 4);
+  const __amdgpu_buffer_rsrc_t rws = make_rsrc(ws, (size_t)O * I * C * 4);
   float mx = 0.0f;
   float wbv[4], scv[4], rows[4][kCp];
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
+  for (int u = 0; u < 4; ++u) {  // a lane with no feature below I writes zeros in pass 2
     wbv[u] = 0.0f;
     scv[u] = 0.0f;
 #pragma unroll
     for (int c = 0; c < kCp; ++c) rows[u][c] = 0.0f;
   }
-  if (col) {
-    for (int f0 = first; f0 < I; f0 += 4 * kStride) {
+  for (int f0 = first; f0 < I; f0 += 4 * kStride) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int f = f0 + u * kStride;
-        wbv[u] = 0.0f;
-        scv[u] = 0.0f;
+    for (int u = 0; u < 4; ++u) {
+      const int f = f0 + u * kStride;
+      const bool ok = col && f < I;
+      const unsigned off = ok ? (unsigned)(((size_t)o * I + f) * 4) : kOutOfRange;
+      wbv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rwb, off, 0, 0));
+      scv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, off, 0, 0));
+      const size_t row = ((size_t)o * I + f) * C * 4;
+      if constexpr (vec) {
 #pragma unroll
-        for (int c = 0; c < kCp; ++c) rows[u][c] = 0.0f;
-        if (f < I) {
-          wbv[u] = wb[(size_t)o * I + f];
-          scv[u] = sc[(size_t)o * I + f];
-          spline_row(f, 1.0f, rows[u]);
+        for (int c4 = 0; c4 < kCp / 4; ++c4) {
+          const unsigned o4 = ok && 4 * c4 < C ? (unsigned)(row + 16 * c4) : kOutOfRange;
+          const f32x4 w4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rws, o4, 0, 0));
+#pragma unroll
+          for (int e = 0; e < 4; ++e) rows[u][4 * c4 + e] = w4[e];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < kCp; ++c) {
+          const unsigned o1 = ok && c < C ? (unsigned)(row + 4 * c) : kOutOfRange;
+          rows[u][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rws, o1, 0, 0));
         }
       }
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float m = 0.0f;
+    for (int u = 0; u < 4; ++u) {
+      float m = 0.0f;
 #pragma unroll
-        for (int c = 0; c < kCp; ++c) m = fmaxf(m, fabsf(rows[u][c]));
-        mx = fmaxf(mx, fmaxf(fabsf(wbv[u]), fabsf(scv[u]) * m));
-      }
+      for (int c = 0; c < kCp; ++c) m = fmaxf(m, fabsf(rows[u][c]));
+      mx = fmaxf(mx, fmaxf(fabsf(wbv[u]), fabsf(scv[u]) * m));
     }
   }
   for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
@@ -471,7 +487,7 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
 
 // Four waves per SIMD (at most 128 VGPRs): two workgroups per CU, so 512 column workgroups
 // are resident at once; at 132 VGPRs it was one per CU and twice as slow.
-template <int kCp>
+template <int kCp, bool kVecW>
 __global__ __launch_bounds__(kPackThreads) __attribute__((amdgpu_waves_per_eu(4))) void kan_pack(
     const float* __restrict__ wb, const float* __restrict__ ws, const float* __restrict__ sc, int I,
     int O, int C, int Opad, float* __restrict__ colscale, _Float16* __restrict__ bhi,
@@ -486,7 +502,7 @@ __global__ __launch_bounds__(kPackThreads) __attribute__((amdgpu_waves_per_eu(4)
     if (threadIdx.x == 0) uflags[b] = (uniform ? 1 : 0) | (cardinal ? 2 : 0);
     return;
   }
-  pack_columns<kCp>(t, wb, ws, sc, I, O, C, Opad, colscale, bhi, blo, ngroups, counters, ncounters);
+  pack_columns<kCp, kVecW>(t, wb, ws, sc, I, O, C, Opad, colscale, bhi, blo, ngroups, counters, ncounters);
 }
 
 __device__ __forceinline__ f32x4 mfma16(f16x8 a, f16x8 b, f32x4 c) {
