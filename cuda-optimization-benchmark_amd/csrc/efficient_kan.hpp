@@ -356,9 +356,12 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
   // behind per-run branches the compiler waited for each run's loads before issuing the
   // next run's, one memory round trip per run.  The last four runs stay in registers for
   // pass 2.
-  const __amdgpu_buffer_rsrc_t rwb = make_rsrc(wb, (size_t)O * I * 4);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc, (size_t)O * I * 4);
-  const __amdgpu_buffer_rsrc_t rws = make_rsrc(ws, (size_t)O * I * C * 4);
+  // The descriptors start at this wave's column, so their 32-bit offsets cover any I (Ws as
+  // a whole may pass 2 GiB).  A column past O reads nothing (every offset out of range).
+  const size_t ocol = col ? (size_t)o : 0;
+  const __amdgpu_buffer_rsrc_t rwb = make_rsrc(wb + ocol * I, (size_t)I * 4);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc + ocol * I, (size_t)I * 4);
+  const __amdgpu_buffer_rsrc_t rws = make_rsrc(ws + ocol * I * C, (size_t)I * C * 4);
   float mx = 0.0f;
   float wbv[4], scv[4], rows[4][kCp];
 #pragma unroll
@@ -373,14 +376,14 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
     for (int u = 0; u < 4; ++u) {
       const int f = f0 + u * kStride;
       const bool ok = col && f < I;
-      const unsigned off = ok ? (unsigned)(((size_t)o * I + f) * 4) : kOutOfRange;
+      const unsigned off = ok ? (unsigned)f * 4u : kOutOfRange;
       wbv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rwb, off, 0, 0));
       scv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, off, 0, 0));
-      const size_t row = ((size_t)o * I + f) * C * 4;
+      const unsigned row = (unsigned)f * (unsigned)C * 4u;
       if constexpr (vec) {
 #pragma unroll
         for (int c4 = 0; c4 < kCp / 4; ++c4) {
-          const unsigned o4 = ok && 4 * c4 < C ? (unsigned)(row + 16 * c4) : kOutOfRange;
+          const unsigned o4 = ok && 4 * c4 < C ? row + 16u * c4 : kOutOfRange;
           const f32x4 w4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rws, o4, 0, 0));
 #pragma unroll
           for (int e = 0; e < 4; ++e) rows[u][4 * c4 + e] = w4[e];
@@ -388,7 +391,7 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
       } else {
 #pragma unroll
         for (int c = 0; c < kCp; ++c) {
-          const unsigned o1 = ok && c < C ? (unsigned)(row + 4 * c) : kOutOfRange;
+          const unsigned o1 = ok && c < C ? row + 4u * c : kOutOfRange;
           rows[u][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rws, o1, 0, 0));
         }
       }

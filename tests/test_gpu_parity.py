@@ -180,6 +180,37 @@ def test_efficient_kan_knot_jitter_full_width(lib, jitter, weights):
     assert t["mismatched"] == 0, t
 
 
+def test_efficient_kan_spline_weights_past_2gib(lib):
+    """Ws of more than 2 GiB (O = 4096, I = 16400, C = 8: 2.15e9 bytes) on the fast path,
+    with split-K (16 output tiles).  The weight packing addresses each output column's row
+    of Ws from the row's own start, so the last columns, whose rows lie past 2 GiB, must
+    read their real weights.  Only those 16 columns carry nonzero spline weights, which
+    keeps the fp64 check small: the base term over every column, the spline term over the
+    last 16."""
+    B, I, O, G, K = 8, 16400, 4096, 5, 3
+    C = G + K
+    print(f"\n[parity] efficient_kan B{B} I{I} O{O} G{G}: Ws of {O * I * C * 4} bytes", flush=True)
+    g = torch.Generator().manual_seed(7400)
+    x = torch.rand(B, I, generator=g) * 2.0 - 1.0
+    grid = (torch.arange(-K, G + K + 1, dtype=torch.float32) * (2.0 / G) - 1.0).expand(I, -1).contiguous()
+    wb = torch.randn(O, I, generator=g) * 0.02
+    sc = torch.randn(O, I, generator=g) * 0.1 + 1.0
+    ws = torch.zeros(O, I, C)
+    ws[-16:] = torch.randn(16, I, C, generator=g) * 0.05
+    assert ws.numel() * 4 > 2 ** 31
+    inp = dict(x=x, grid=grid, base_weight=wb, spline_weight=ws, spline_scaler=sc, grid_size=G,
+               spline_order=K, B=B, I=I, O=O)
+    got = capi.run_op(lib, "efficient_kan", inp)["out"].cpu().numpy()
+    xd = x.double().numpy()
+    want = (xd / (1.0 + np.exp(-xd))) @ wb.double().numpy().T
+    bases = exact.b_splines(xd, grid.double().numpy(), K)
+    w16 = (ws[-16:].double() * sc[-16:].double()[:, :, None]).reshape(16, -1).numpy()
+    want[:, -16:] += bases.reshape(B, -1) @ w16.T
+    t = tally(got, want, tasks.load_task("efficient_kan")["tolerance"])
+    print(f"[parity] worst error {t['worst']:.4f} of the tolerance", flush=True)
+    assert t["mismatched"] == 0, t
+
+
 # (M, K, N, output offset in bf16 elements).  K % 16 == 0 with 16-byte aligned operands
 # runs the wide kernel: its three epilogues (N % 8 == 0 and a 16-byte aligned output; N % 4
 # == 0 and 8-byte aligned; otherwise), M and N tile tails, K not a multiple of its 128-wide
