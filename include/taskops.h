@@ -112,8 +112,10 @@ hipError_t taskops_ppo_clip_entropy_noalloc(int32_t B, int32_t T, int32_t H,
  * nonzero entries of base_weight and spline_weight*spline_scaler span at most about 2^24
  * in magnitude (smaller ones lose bits to the fp16 low halves); knot rows uniform to
  * 5e-7 h use the cardinal cubic pieces (about 1e-6 of a basis value from the exact bases),
- * all other rows exact per-interval cubics.  Other orders and knot counts take an fp32
- * row-wise path without these limits.
+ * all other rows exact per-interval cubics.  It also needs x, out, its packed weights and
+ * one output column's I x 16 spline slots each under 2 GiB (spline_weight as a whole may be
+ * larger).  Other orders, knot counts and sizes take an fp32 row-wise path without these
+ * limits.
  * Replaces: reference/efficient_kan/solution.cu:177-288
  *           (tasks/efficient_kan/tests/task.json:3; op: reference.py:33-51). */
 hipError_t taskops_efficient_kan(const float* x, const float* grid, const float* base_weight,
