@@ -159,6 +159,9 @@ hipError_t workspace(WorkspaceSlot slot, size_t bytes, hipStream_t stream, void*
 // Number of compute units of the current device (cached per device).
 int device_cu_count();
 
+// LDS bytes per compute unit of the current device (cached per device).
+int device_lds_per_cu();
+
 // Workgroup barrier without __syncthreads()'s release fence: that fence waits for every
 // outstanding vector memory operation (vmcnt(0)), which would drain the copy ring at each
 // step.  Callers account for their copies with explicit vmcnt waits; LDS reads issued

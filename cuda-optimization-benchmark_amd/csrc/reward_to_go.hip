@@ -17,15 +17,26 @@ namespace {
 constexpr int kPerLane = 4;
 constexpr int kNonTemporal = 5;  // non-temporal loads (bit 0) and stores (policy 2 in bits 1-2)
 
+// Rows of 4 waves x 4 chunks (T > 2048) run with at most this many workgroups per CU,
+// held there by the LDS each one reserves (the kernel's own LDS is a few bytes).  At the
+// kernel's 68 VGPRs the registers allow 7; 4 measured fastest at B = T = 4096 (25.53
+// against 25.76 us per call, 5 and 6 slower, 3 slower still) and at B = 3000 (20.15 against
+// 20.63 us), and the same at B = 8192 and 1024 (one MI355X, cold rotating inputs).
+constexpr int kLongRowWorkgroupsPerCU = 4;
+
+// Dynamic LDS that lets at most `per_cu` workgroups share a CU: more than 1/(per_cu+1) of it.
+size_t occupancy_lds(int per_cu) { return (size_t)device_lds_per_cu() / (per_cu + 1) + 1; }
+
 template <int kWaves, int kSeg>
 void launch(const float* reward, const uint8_t* done, double g, int B, int T, float* out,
             bool vec, hipStream_t stream) {
+  const size_t lds = (kWaves == 4 && kSeg == 4) ? occupancy_lds(kLongRowWorkgroupsPerCU) : 0;
   if (vec)
     hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, true, kNonTemporal>), dim3(B),
-                       dim3(kWaves * kWave), 0, stream, reward, done, g, B, T, out);
+                       dim3(kWaves * kWave), lds, stream, reward, done, g, B, T, out);
   else
     hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, false, kNonTemporal>), dim3(B),
-                       dim3(kWaves * kWave), 0, stream, reward, done, g, B, T, out);
+                       dim3(kWaves * kWave), lds, stream, reward, done, g, B, T, out);
 }
 
 }  // namespace

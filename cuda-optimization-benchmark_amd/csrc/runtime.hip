@@ -20,6 +20,7 @@ Region g_regions[kMaxDevices][kNumSlots];
 // the replacement may still be using them, and freeing would need a host sync.
 std::vector<void*> g_retired;
 int g_cus[kMaxDevices] = {0};
+int g_lds_per_cu[kMaxDevices] = {0};
 
 // Zero fill as a kernel rather than hipMemsetAsync: no library call enqueues memset work,
 // which keeps memset nodes out of any graph a caller captures.
@@ -74,6 +75,17 @@ int device_cu_count() {
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
     n = 256;
   __atomic_store_n(&g_cus[dev], n, __ATOMIC_RELAXED);
+  return n;
+}
+
+int device_lds_per_cu() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 160 * 1024;
+  int n = __atomic_load_n(&g_lds_per_cu[dev], __ATOMIC_RELAXED);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess || n <= 0)
+    n = 160 * 1024;
+  __atomic_store_n(&g_lds_per_cu[dev], n, __ATOMIC_RELAXED);
   return n;
 }
 
