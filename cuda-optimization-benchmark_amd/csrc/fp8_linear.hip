@@ -56,7 +56,7 @@ extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const 
     if (2 * tiles <= device_cu_count()) {
       // At most half a 256x256 tile per CU: 128x256 tiles, twice as many workgroups.
       const dim3 hgrid(((M + kHalfRows - 1) / kHalfRows) * ((N + BN - 1) / BN));
-      const size_t half_lds = kHalfLdsBytes;
+      const size_t half_lds = kHalfLaunchLdsBytes;
       if (N % 8 == 0 && (o & 15) == 0)
         hipLaunchKernelGGL(fp8_gemm_half<2>, hgrid, dim3(kThreads), half_lds, stream, x_fp8, w_fp8, (int)M,
                            (int)N, (int)K, inv, bias, output);

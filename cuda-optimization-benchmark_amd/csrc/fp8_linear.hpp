@@ -559,7 +559,9 @@ constexpr int kHalfXDma = kHalfRows / 8 / (kThreads / kWave);       // x copies 
 constexpr int kHalfCopies = kHalfXDma + kWideDmaPerWave;             // 12
 constexpr int kHalfParts = 2 * (4 + kHalfMI);                        // 16-byte reads per half step: 12
 constexpr int kHalfSlots = 4 * kHalfMI;                              // MFMAs per half step: 8
-static_assert(kHalfRows * kTileRowBytes + kBiasBytes <= kHalfLdsBytes, "the output tile and bias fit the rings");
+static_assert(kHalfRows * kTileRowBytes <= kHalfLdsBytes, "the output tile fits the rings");
+// The bias sits past the rings, where no copy lands.
+constexpr int kHalfLaunchLdsBytes = kHalfLdsBytes + kBiasBytes;  // 144.5 KiB
 static_assert(kHalfCopies % 2 == 0, "each half step issues half the copies");
 
 // Group `group` (8 rows) of a tile with 128-byte rows: one direct-to-LDS instruction.
@@ -612,12 +614,16 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
                  : frag128_part(a_tile(step), arow + 32 * ((p - 8) / 2), fg, half, p % 2);
   };
 
-  // Prologue: steps 0 and 1, then step 0's first-half fragments.
+  // Prologue: the bias (staged past the rings, so its load overlaps the first copies'),
+  // steps 0 and 1, then step 0's first-half fragments.
+  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
 #pragma unroll
   for (int c = 0; c < kHalfCopies; ++c) copy(0, c);
 #pragma unroll
   for (int c = 0; c < kHalfCopies; ++c) copy(1, c);
   wait_vmcnt<kHalfCopies>();
+  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + kHalfLdsBytes);
+  bias_s[tid] = bias_v;
   __syncthreads();
   i32x8 a0[kHalfMI], b0[4], a1[kHalfMI], b1[4];
 #pragma unroll
@@ -658,14 +664,9 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
     // Second half: MFMAs on step kt's second 64 k, reading step kt+1's first 64 k.
     half_step(a1, b1, a0, b0, kt, kHalfCopies / 2, kt + 1, 0);
   }
-  const unsigned short bias_v = load_bias(bias, n0, rows_b, tid);
-  // bias_s lies in w ring slot 0, where the zero-filling copies of step nk+1 land when
-  // nk % 3 == 2 (K = 1024), and each wave's vmcnt covers only its own copies: every wave
-  // drains its copies and passes a barrier before any wave writes the bias there.
+  // The output tile is staged in the rings: every wave drains its own copies (the
+  // zero-filling ones past K included) and passes a barrier before any wave writes there.
   wait_vmcnt<0>();
-  __syncthreads();
-  uint16_t* bias_s = reinterpret_cast<uint16_t*>(smem + kHalfRows * kTileRowBytes);
-  bias_s[tid] = bias_v;
   __syncthreads();
   int et = tid;
   asm volatile("" : "+v"(et));
@@ -776,6 +777,12 @@ __global__ __launch_bounds__(kSkinnyThreads) void fp8_gemm_skinny_flat(
   const __amdgpu_buffer_rsrc_t wb = make_rsrc(w + (size_t)n0 * K, (size_t)rows_w * K);
   const __amdgpu_buffer_rsrc_t xa = make_rsrc(x, (size_t)M * K);
   const int lr = lane / kChunks, p = lane % kChunks;  // row within a load, chunk
+  // Every output this thread finishes is in column n0 + tid % 16 (the epilogue's stride is
+  // a multiple of 16), so its bias is loaded now and its latency overlaps the K loop's.
+  const int bc = (int)threadIdx.x % 16;
+  const __amdgpu_buffer_rsrc_t rbias = make_rsrc(bias + n0, (size_t)rows_w * 2);
+  const float bias_v = bf16_to_f32(
+      __builtin_amdgcn_raw_buffer_load_b16(rbias, bc < rows_w ? (unsigned)bc * 2u : kOutOfRange, 0, 0));
   f32x4 acc[kRB];
 #pragma unroll
   for (int i = 0; i < kRB; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -821,7 +828,7 @@ __global__ __launch_bounds__(kSkinnyThreads) void fp8_gemm_skinny_flat(
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < kSkinnyWaves; ++q) s += part[(q * 16 * kRB + m) * 16 + c];
-    out[(size_t)m * N + n] = f32_to_bf16_rne(s * inv_scale + bf16_to_f32(bias[n]));
+    out[(size_t)m * N + n] = f32_to_bf16_rne(s * inv_scale + bias_v);
   }
 }
 
