@@ -10,12 +10,27 @@
 using namespace taskops;
 using namespace taskops::fp8;
 
+namespace {
+
+// True when every 32-bit buffer offset of the kernels fits: a workgroup addresses its
+// operand rows (at most 256 rows of K bytes above M = 64; all M rows of x and 16 of w in
+// the skinny kernels) and, above M = 64, its output rows (at most 256 rows of N bf16
+// values) through descriptors of at most 2^31 - 1 bytes.
+bool offsets_fit(int64_t M, int64_t K, int64_t N) {
+  const int64_t lim = 0x7fffffff;
+  if (M <= kSkinnyMaxM) return M * K <= lim && 16 * K <= lim;
+  return (int64_t)BM * K <= lim && (int64_t)BM * N * 2 <= lim;
+}
+
+}  // namespace
+
 extern "C" hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_fp8,
                                          float scale_x, const uint8_t* w_fp8, float scale_w,
                                          const uint16_t* bias, uint16_t* output,
                                          hipStream_t stream) {
   if (M < 0 || K < 0 || N < 0) return hipErrorInvalidValue;
   if (M == 0 || N == 0) return hipSuccess;
+  if (!offsets_fit(M, K, N)) return hipErrorInvalidValue;
   const float inv = (float)(1.0 / ((double)scale_x * (double)scale_w));
   const int vec = vec_width(x_fp8, w_fp8, K);
   if (M <= kSkinnyMaxM) {

@@ -49,7 +49,8 @@ extern "C" hipError_t taskops_reward_to_go(const float* reward, const bool* done
                                            hipStream_t stream) {
   if (B <= 0 || T <= 0) return hipSuccess;  // nothing to write
   const uint8_t* d = reinterpret_cast<const uint8_t*>(done);
-  const bool vec = (T % 4) == 0 &&
+  // The vector path's buffer stores address a row in 32-bit bytes (store_row16).
+  const bool vec = (T % 4) == 0 && T < (1 << 30) &&
                    ((reinterpret_cast<uintptr_t>(reward) | reinterpret_cast<uintptr_t>(output)) & 15) == 0 &&
                    (reinterpret_cast<uintptr_t>(d) & 3) == 0;
   const int nchunks = (T + kWave * kPerLane - 1) / (kWave * kPerLane);  // chunks of 256 steps

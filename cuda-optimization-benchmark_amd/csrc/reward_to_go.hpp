@@ -60,10 +60,12 @@ __device__ __forceinline__ float coef32(unsigned word, int byte, float g) {
 // policy pays depends on the access pattern: with 4 steps per lane (whole 1 KiB per store
 // instruction) nt stores are the fastest, with 8 steps per lane (every other 16 bytes)
 // they are the slowest (reward_to_go.hip).
+// The descriptor spans the row, so T * 4 bytes must fit its 32-bit size: the host takes
+// rows of 2^30 steps or more down the element path.
 template <int kStorePolicy>  // bit 0 sc0, bit 1 nt
 __device__ __forceinline__ void store_row16(float* row_base, int T, int t, f32x4 w) {
   const __amdgpu_buffer_rsrc_t rs =
-      __builtin_amdgcn_make_buffer_rsrc(row_base, (short)0, T * 4, 0x00020000);
+      __builtin_amdgcn_make_buffer_rsrc(row_base, (short)0, (int)((unsigned)T * 4u), 0x00020000);
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned, w), rs,
                                          (unsigned)t * 4u, 0, kStorePolicy);
 }

@@ -61,7 +61,7 @@ hipError_t taskops_leaky(const float* input_current, const float* mem0, const fl
 
 /* output[b,t] = reward[b,t] + gamma * (done[b,t] ? 0 : output[b,t+1]), output[b,T] = 0.
  * Affine scan carried in fp64, one rounding to fp32 per element.  B <= 0 or T <= 0 does
- * nothing.
+ * nothing.  Any T up to INT32_MAX; rows of 2^30 steps or more take the element-wise path.
  * Replaces: reference/reward_to_go/solution.cu:237-264
  *           (tasks/reward_to_go/tests/task.json:3; op: reference.py:34-42). */
 hipError_t taskops_reward_to_go(const float* reward, const bool* done, float gamma,
@@ -125,7 +125,10 @@ hipError_t taskops_efficient_kan(const float* x, const float* grid, const float*
 
 /* FP8 (OCP e4m3) linear: output[M,N] = bf16( (x/scale_x) @ (w/scale_w)^T + bias ),
  * x [M,K] and w [N,K] row-major e4m3 bytes, bias [N] bf16, fp32 accumulation, one
- * round-to-nearest-even to bf16.
+ * round-to-nearest-even to bf16.  A workgroup addresses its rows with 32-bit offsets, so
+ * shapes past them return hipErrorInvalidValue and write nothing: for M > 64, K above
+ * 8,388,607 or N above 4,194,303; for M <= 64, M*K or 16*K above 2^31 - 1.  Negative
+ * sizes return hipErrorInvalidValue; M == 0 or N == 0 does nothing.
  * Replaces: reference/fp8_linear/solution.cu:276-321 (tasks/fp8_linear/tests/task.json:3;
  *           op: tasks/fp8_linear/reference.py:34-41). */
 hipError_t taskops_fp8_linear(int32_t M, int32_t K, int32_t N, const uint8_t* x_fp8,

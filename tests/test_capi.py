@@ -50,6 +50,29 @@ def test_planted_exports(op):
     assert hasattr(lib, "grader_entry") and hasattr(lib, "planted_select")
 
 
+HIP_ERROR_INVALID_VALUE = 1
+
+
+@pytest.mark.parametrize("M,K,N", [
+    (65, 8_388_608, 16),        # a 256-row operand panel of K bytes passes 2^31 - 1
+    (4096, 1 << 24, 4096),
+    (65, 16, 4_194_304),        # a 256-row output panel of N bf16 values passes 2^31 - 1
+    (64, 33_554_432, 16),       # the skinny kernel's x (M rows of K bytes)
+    (1, 134_217_728, 16),       # the skinny kernel's 16 w rows
+    (-1, 16, 16), (16, -1, 16), (16, 16, -1),
+])
+def test_fp8_linear_refuses_shapes_past_its_offsets(M, K, N):
+    """Argument checks run before any HIP call, so they are testable without a GPU: shapes
+    whose per-workgroup rows the kernels' 32-bit buffer offsets cannot address are refused
+    (hipErrorInvalidValue), never computed wrongly."""
+    lib = capi.load()
+    f = lib.taskops_fp8_linear
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_float,
+                  ctypes.c_void_p, ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    assert f(M, K, N, None, 1.0, None, 1.0, None, None, None) == HIP_ERROR_INVALID_VALUE
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(capi.TaskOpsError):
         capi.load(tmp_path / "libtaskops.so")
