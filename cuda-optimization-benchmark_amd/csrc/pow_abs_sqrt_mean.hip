@@ -12,6 +12,9 @@ constexpr int kThreads = 256;
 constexpr int kUnroll = 2;
 constexpr int kBlocksPerCU = 2;
 constexpr bool kNonTemporal = true;
+// Elements per call at most: 2^40 (4 TiB per fp32 input, far beyond one GPU's memory), so
+// batch_size * 4 * height * width is formed without overflowing int64.
+constexpr int64_t kMaxElements = int64_t(1) << 40;
 
 __global__ void write_nan_kernel(float* out) { out[0] = __builtin_nanf(""); }
 
@@ -25,7 +28,10 @@ extern "C" hipError_t taskops_pow_abs_sqrt_mean(const float* inp, const float* t
                                                 int64_t width, float* output,
                                                 hipStream_t stream) {
   if (batch_size < 0 || height < 0 || width < 0) return hipErrorInvalidValue;
-  const int64_t n = batch_size * 4 * height * width;
+  int64_t n = 0;
+  if (__builtin_mul_overflow(batch_size, (int64_t)4, &n) || __builtin_mul_overflow(n, height, &n) ||
+      __builtin_mul_overflow(n, width, &n) || n > kMaxElements)
+    return hipErrorInvalidValue;
   if (n == 0) {
     hipLaunchKernelGGL(write_nan_kernel, dim3(1), dim3(1), 0, stream, output);
     return hipGetLastError();

@@ -41,8 +41,8 @@ int taskops_version(void);
 
 /* output[0] = mean over n = batch_size*4*height*width elements of
  * sqrt((inp - target)^2 + 1e-6), fp32 result of an fp64 reduction.  n == 0 writes NaN
- * (the mean of nothing, as reference_exact gives); a negative dimension returns
- * hipErrorInvalidValue and writes nothing.
+ * (the mean of nothing, as reference_exact gives); a negative dimension, or n above 2^40,
+ * returns hipErrorInvalidValue and writes nothing.
  * Replaces: reference/pow_abs_sqrt_mean/solution.cu:99-118
  *           (tasks/pow_abs_sqrt_mean/tests/task.json:3; op: reference.py:22-28). */
 hipError_t taskops_pow_abs_sqrt_mean(const float* inp, const float* target,

@@ -73,6 +73,19 @@ def test_fp8_linear_refuses_shapes_past_its_offsets(M, K, N):
     assert f(M, K, N, None, 1.0, None, 1.0, None, None, None) == HIP_ERROR_INVALID_VALUE
 
 
+@pytest.mark.parametrize("dims", [(-1, 1, 1), (1, -1, 1), (1 << 20, 1 << 20, 1), (1 << 40, 1 << 40, 1 << 40),
+                                  ((1 << 62), 4, 1)])
+def test_pow_refuses_sizes_past_2_40(dims):
+    """batch_size * 4 * height * width above 2^40 (or overflowing int64) is refused before
+    any HIP call, never formed with a wrapped product."""
+    lib = capi.load()
+    f = lib.taskops_pow_abs_sqrt_mean
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
+                  ctypes.c_void_p, ctypes.c_void_p]
+    assert f(None, None, *dims, None, None) == HIP_ERROR_INVALID_VALUE
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(capi.TaskOpsError):
         capi.load(tmp_path / "libtaskops.so")
