@@ -27,6 +27,8 @@ extern "C" hipError_t taskops_leaky(const float* input_current, const float* mem
   int vec = 1;
   if (H % 2 == 0 && (bits & 7) == 0) vec = 2;
   const int64_t threads = N / vec;
+  // One launch covers at most 2^32 - 1 work-items: B*H up to 2^32 - 256 neurons on either path.
+  if (N > (int64_t(1) << 32) - kThreads) return hipErrorInvalidValue;
   const unsigned blocks = (unsigned)((threads + kThreads - 1) / kThreads);
   if (vec == 2)
     hipLaunchKernelGGL((leaky_kernel<kThreads, 2, kDepth, kNonTemporal>), dim3(blocks), dim3(kThreads), 0,

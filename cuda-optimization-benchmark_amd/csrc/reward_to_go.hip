@@ -27,16 +27,24 @@ constexpr int kLongRowWorkgroupsPerCU = 4;
 // Dynamic LDS that lets at most `per_cu` workgroups share a CU: more than 1/(per_cu+1) of it.
 size_t occupancy_lds(int per_cu) { return (size_t)device_lds_per_cu() / (per_cu + 1) + 1; }
 
+// One workgroup per row, and one launch covers at most 2^32 - 1 work-items in a dimension,
+// so rows go out in launches of at most kRowsPerLaunch (one launch for every B up to it).
+constexpr int kRowsPerLaunch = 1 << 23;
+
 template <int kWaves, int kSeg>
 void launch(const float* reward, const uint8_t* done, double g, int B, int T, float* out,
             bool vec, hipStream_t stream) {
   const size_t lds = (kWaves == 4 && kSeg == 4) ? occupancy_lds(kLongRowWorkgroupsPerCU) : 0;
-  if (vec)
-    hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, true, kNonTemporal>), dim3(B),
-                       dim3(kWaves * kWave), lds, stream, reward, done, g, B, T, out);
-  else
-    hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, false, kNonTemporal>), dim3(B),
-                       dim3(kWaves * kWave), lds, stream, reward, done, g, B, T, out);
+  for (int b0 = 0; b0 < B; b0 += kRowsPerLaunch) {
+    const int nb = B - b0 < kRowsPerLaunch ? B - b0 : kRowsPerLaunch;
+    const size_t off = (size_t)b0 * (size_t)T;  // T % 4 == 0 on the vector path: alignment kept
+    if (vec)
+      hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, true, kNonTemporal>), dim3(nb),
+                         dim3(kWaves * kWave), lds, stream, reward + off, done + off, g, nb, T, out + off);
+    else
+      hipLaunchKernelGGL((reward_to_go_kernel<kWaves, kPerLane, kSeg, false, kNonTemporal>), dim3(nb),
+                         dim3(kWaves * kWave), lds, stream, reward + off, done + off, g, nb, T, out + off);
+  }
 }
 
 }  // namespace

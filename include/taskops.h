@@ -52,7 +52,8 @@ hipError_t taskops_pow_abs_sqrt_mean(const float* inp, const float* target,
 /* Leaky integrate-and-fire layer, reset by subtraction, T steps over B*H neurons.
  * beta is clamped to [0,1]; per step: reset = (mem >= th); mem = beta*mem + x[t] - reset*th
  * (each operation rounded in fp32, no contraction); spikes[t] = (mem >= th).
- * Bit-identical to the fp32 step-by-step reference.
+ * Bit-identical to the fp32 step-by-step reference.  Negative sizes, or B*H above
+ * 2^32 - 256 neurons (one launch's work-items), return hipErrorInvalidValue.
  * Replaces: reference/leaky/solution.cu:106-138 (tasks/leaky/tests/task.json:3;
  *           op: tasks/leaky/reference.py:26-37). */
 hipError_t taskops_leaky(const float* input_current, const float* mem0, const float* beta,

@@ -86,6 +86,16 @@ def test_pow_refuses_sizes_past_2_40(dims):
     assert f(None, None, *dims, None, None) == HIP_ERROR_INVALID_VALUE
 
 
+@pytest.mark.parametrize("T,B,H", [(-1, 1, 1), (1, -1, 1), (1, 1, -1), (1, 65536, 65536), (1, 65535, 65537)])
+def test_leaky_refuses_more_neurons_than_one_launch(T, B, H):
+    """B*H above 2^32 - 256 neurons (one launch's work-items) is refused before any HIP call."""
+    lib = capi.load()
+    f = lib.taskops_leaky
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_void_p] * 4 + [ctypes.c_int32] * 3 + [ctypes.c_void_p] * 3
+    assert f(None, None, None, None, T, B, H, None, None, None) == HIP_ERROR_INVALID_VALUE
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(capi.TaskOpsError):
         capi.load(tmp_path / "libtaskops.so")

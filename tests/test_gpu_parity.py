@@ -423,6 +423,21 @@ def test_grid_reduction_sizes(lib, grid):
 RTG_T = [1, 255, 256, 257, 511, 512, 513, 1023, 1024, 1025, 1500, 2048, 2049, 4095, 4096, 4097, 9000]
 
 
+@pytest.mark.parametrize("T", [4, 5])
+def test_reward_to_go_rows_past_one_launch(lib, T):
+    """More rows than one launch takes (2^23, one workgroup per row): the rows go out in two
+    launches, the second starting at row 2^23 (T = 4 on the vector path, T = 5 on the element
+    path)."""
+    B = (1 << 23) + 3
+    print(f"\n[parity] reward_to_go B={B} T={T}", flush=True)
+    case = dict(name="rows", seed=77 + T, B=B, T=T, gamma=0.97, done_p=0.1)
+    inp = inputs.make_inputs("reward_to_go", case)
+    want = exact.reward_to_go(inp)["output"]
+    got = capi.run_op(lib, "reward_to_go", inp)["output"].cpu()
+    t = tally(got, want, tasks.load_task("reward_to_go")["tolerance"])
+    assert t["mismatched"] == 0 and t["unwritten"] == 0, t
+
+
 @pytest.mark.parametrize("T", RTG_T)
 def test_reward_to_go_lengths(lib, T):
     print(f"\n[parity] reward_to_go T={T}", flush=True)
