@@ -37,8 +37,8 @@ __global__ __launch_bounds__(kRowThreads) void kan_rowwise(
     float* __restrict__ out) {
   extern __shared__ float lds[];  // [kFeat][1 + C]
   const int L = G + 2 * order + 1, C = G + order, S = 1 + C;
-  const int b = blockIdx.y;
-  const int o = blockIdx.x * kRowThreads + threadIdx.x;
+  const int b = blockIdx.x;  // batch rows along x, whose grid limit is 2^31 - 1
+  const int o = blockIdx.y * kRowThreads + threadIdx.x;
   float acc = 0.0f;
   for (int i0 = 0; i0 < I; i0 += kFeat) {
     const int nf = min(kFeat, I - i0);
@@ -153,7 +153,7 @@ extern "C" hipError_t taskops_efficient_kan(const float* x, const float* grid,
     return launch_fast<16>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
   }
   const int S = 1 + C;
-  dim3 g((O + kRowThreads - 1) / kRowThreads, B);
+  dim3 g(B, (O + kRowThreads - 1) / kRowThreads);
   hipLaunchKernelGGL(kan_rowwise, g, dim3(kRowThreads), (size_t)kFeat * S * sizeof(float), stream, x,
                      grid, base_weight, spline_weight, spline_scaler, (int)grid_size,
                      (int)spline_order, (int)I, (int)O, out);
