@@ -97,6 +97,27 @@ def test_gpu_quantize_sizes(lib, n):
     assert np.array_equal(q, q_want)
 
 
+def _random_quantize_cases(count=24, seed=20261203):
+    """Seeded draws: size log-uniform over 1 .. 3M, x and q offsets (unaligned ones take the
+    two-pass path), and the values' magnitude."""
+    import random
+    rng = random.Random(seed)
+    return [(int(10 ** rng.uniform(0, 6.5)), rng.choice([0, 0, 1, 3]), rng.choice([0, 0, 1, 2, 3]),
+             rng.choice([1e-6, 1.0, 7.0, 1e4])) for _ in range(count)]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("n,x_off,q_off,mag", _random_quantize_cases())
+def test_gpu_quantize_random(lib, n, x_off, q_off, mag):
+    """Random sizes, offsets and magnitudes: the codes and the scale equal the oracle's."""
+    print(f"\n[parity] quantize_e4m3 random n={n} x_off={x_off} q_off={q_off} mag={mag}", flush=True)
+    x = torch.randn(n, generator=torch.Generator().manual_seed(n + 17 * x_off + q_off)) * mag
+    q, s = _run_gpu(lib, x, q_off=q_off, x_off=x_off)
+    q_want, s_want = e4m3.quantize(x.numpy())
+    assert s == s_want
+    assert e4m3.same_codes(q, q_want)
+
+
 @pytest.mark.gpu
 def test_gpu_quantize_cast_table(lib):
     """Every e4m3 value, midpoint and neighbour with scale exactly 1 (|x| max = 448): the
