@@ -153,9 +153,15 @@ extern "C" hipError_t taskops_efficient_kan(const float* x, const float* grid,
     return launch_fast<16>(x, grid, base_weight, spline_weight, spline_scaler, C, B, I, O, L, out, stream);
   }
   const int S = 1 + C;
-  dim3 g(B, (O + kRowThreads - 1) / kRowThreads);
-  hipLaunchKernelGGL(kan_rowwise, g, dim3(kRowThreads), (size_t)kFeat * S * sizeof(float), stream, x,
-                     grid, base_weight, spline_weight, spline_scaler, (int)grid_size,
-                     (int)spline_order, (int)I, (int)O, out);
+  // One workgroup per batch row and output block; a launch covers at most 2^32 - 1
+  // work-items along x, so batch rows go out 2^23 at a time.
+  constexpr int kRowsPerLaunch = 1 << 23;
+  for (int b0 = 0; b0 < B; b0 += kRowsPerLaunch) {
+    const int nb = B - b0 < kRowsPerLaunch ? B - b0 : kRowsPerLaunch;
+    dim3 g(nb, (O + kRowThreads - 1) / kRowThreads);
+    hipLaunchKernelGGL(kan_rowwise, g, dim3(kRowThreads), (size_t)kFeat * S * sizeof(float), stream,
+                       x + (size_t)b0 * I, grid, base_weight, spline_weight, spline_scaler, (int)grid_size,
+                       (int)spline_order, (int)I, (int)O, out + (size_t)b0 * O);
+  }
   return hipGetLastError();
 }

@@ -15,10 +15,13 @@ namespace {
 // True when every 32-bit buffer offset of the kernels fits: a workgroup addresses its
 // operand rows (at most 256 rows of K bytes above M = 64; all M rows of x and 16 of w in
 // the skinny kernels) and, above M = 64, its output rows (at most 256 rows of N bf16
-// values) through descriptors of at most 2^31 - 1 bytes.
+// values) through descriptors of at most 2^31 - 1 bytes.  The skinny grid (16 columns per
+// workgroup of kSkinnyThreads) also stays within one launch's 2^32 - 1 work-items; above
+// M = 64 the offsets bound N, which keeps that grid far inside it.
 bool offsets_fit(int64_t M, int64_t K, int64_t N) {
   const int64_t lim = 0x7fffffff;
-  if (M <= kSkinnyMaxM) return M * K <= lim && 16 * K <= lim;
+  if (M <= kSkinnyMaxM)
+    return M * K <= lim && 16 * K <= lim && (N + 15) / 16 * kSkinnyThreads <= (int64_t)0xffffffff;
   return (int64_t)BM * K <= lim && (int64_t)BM * N * 2 <= lim;
 }
 

@@ -128,7 +128,8 @@ hipError_t taskops_efficient_kan(const float* x, const float* grid, const float*
  * x [M,K] and w [N,K] row-major e4m3 bytes, bias [N] bf16, fp32 accumulation, one
  * round-to-nearest-even to bf16.  A workgroup addresses its rows with 32-bit offsets, so
  * shapes past them return hipErrorInvalidValue and write nothing: for M > 64, K above
- * 8,388,607 or N above 4,194,303; for M <= 64, M*K or 16*K above 2^31 - 1.  Negative
+ * 8,388,607 or N above 4,194,303; for M <= 64, M*K or 16*K above 2^31 - 1, or N above
+ * 134,217,727 (one launch's work-items).  Negative
  * sizes return hipErrorInvalidValue; M == 0 or N == 0 does nothing.
  * Replaces: reference/fp8_linear/solution.cu:276-321 (tasks/fp8_linear/tests/task.json:3;
  *           op: tasks/fp8_linear/reference.py:34-41). */

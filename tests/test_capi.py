@@ -59,6 +59,7 @@ HIP_ERROR_INVALID_VALUE = 1
     (65, 16, 4_194_304),        # a 256-row output panel of N bf16 values passes 2^31 - 1
     (64, 33_554_432, 16),       # the skinny kernel's x (M rows of K bytes)
     (1, 134_217_728, 16),       # the skinny kernel's 16 w rows
+    (1, 16, 134_217_728),       # the skinny grid: 512 threads per 16 columns pass 2^32 - 1
     (-1, 16, 16), (16, -1, 16), (16, 16, -1),
 ])
 def test_fp8_linear_refuses_shapes_past_its_offsets(M, K, N):

@@ -120,8 +120,10 @@ KAN_SHAPES = [
     (64, 96, 40, 8, 3, 1.0, "mixed_edge"),
     (21, 40, 50, 6, 2, 1.2, "random"),
     (16, 12, 8, 13, 1, 1.0, "uniform"),
-    # Row-wise path with more batch rows than a grid's y dimension takes (65,536).
+    # Row-wise path with more batch rows than a grid's y dimension takes (65,536), and with
+    # more than one launch's 2^23 rows.
     (70001, 3, 5, 4, 2, 1.0, "uniform"),
+    ((1 << 23) + 5, 1, 3, 3, 2, 1.0, "uniform"),
     # Split-K (fewer output tiles than CUs): 64 tiles and 5 feature groups split 2+2+1;
     # 96 tiles, ragged O and 3 groups split 2+1.
     (4096, 160, 512, 8, 3, 1.0, "uniform"),
