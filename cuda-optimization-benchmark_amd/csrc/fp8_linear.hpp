@@ -455,8 +455,10 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
   // MFMAs would make the compiler copy the accumulators).
   auto a_tile = [&](int step) { return smem + (step % 3) * kWideOperandBytes; };
   auto b_tile = [&](int step) { return smem + (3 + (step & 1)) * kWideOperandBytes; };
-  auto copy_a = [&](int step, int g0, int n) { dma_tile128(xa, a_tile(step), rows_a, K, step * WBK, wave, lane, g0, n); };
-  auto copy_b = [&](int step, int g0, int n) { dma_tile128(wb, b_tile(step), rows_b, K, step * WBK, wave, lane, g0, n); };
+  // The wave index as a scalar: each copy's LDS destination (M0) is then scalar arithmetic.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  auto copy_a = [&](int step, int g0, int n) { dma_tile128(xa, a_tile(step), rows_a, K, step * WBK, wave_s, lane, g0, n); };
+  auto copy_b = [&](int step, int g0, int n) { dma_tile128(wb, b_tile(step), rows_b, K, step * WBK, wave_s, lane, g0, n); };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * WM + fr, brow = wn * WN + fr;
 
@@ -599,12 +601,14 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
   // As in fp8_gemm_wide, copies past the last step zero-fill a free slot.
   auto a_tile = [&](int step) { return smem + (step % 3) * kHalfXBytes; };
   auto b_tile = [&](int step) { return smem + 3 * kHalfXBytes + (step % 3) * kWideOperandBytes; };
-  // Copy c (0 .. 11) of this wave for `step`: x groups first, then w groups.
+  // Copy c (0 .. 11) of this wave for `step`: x groups first, then w groups.  The wave
+  // index is a scalar, so each copy's LDS destination (M0) is scalar arithmetic.
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto copy = [&](int step, int c) {
     if (c < kHalfXDma)
-      dma_group128(xa, a_tile(step), rows_a, K, step * WBK, wave * kHalfXDma + c, lane);
+      dma_group128(xa, a_tile(step), rows_a, K, step * WBK, wave_s * kHalfXDma + c, lane);
     else
-      dma_group128(wb, b_tile(step), rows_b, K, step * WBK, wave * kWideDmaPerWave + c - kHalfXDma, lane);
+      dma_group128(wb, b_tile(step), rows_b, K, step * WBK, wave_s * kWideDmaPerWave + c - kHalfXDma, lane);
   };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * 32 * kHalfMI + fr, brow = wn * WN + fr;
