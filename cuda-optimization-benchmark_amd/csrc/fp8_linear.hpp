@@ -396,7 +396,19 @@ constexpr int kWideDmaPerWave = (BM * WBK / 16) / kSlotsPerInst / (kThreads / kW
 
 __device__ __forceinline__ int swz128(int row) { return (row >> 1) & 7; }
 
+// Byte offset of (row, gk) in a tile's descriptor for a 16-byte copy, or kOutOfRange.  With
+// kK128 (K % 128 == 0) a step never straddles K, so no per-lane test is needed: rows past the
+// tile lie past the descriptor's end and read zeros, and a step wholly past K only fills a
+// slot that no MFMA uses (its offsets stay below 256 K + 384, inside 32 bits).
+template <bool kK128>
+__device__ __forceinline__ unsigned copy_offset(int row, int rows, int gk, int K) {
+  const unsigned off = (unsigned)row * (unsigned)K + (unsigned)gk;
+  if constexpr (kK128) return off;
+  return (row < rows && gk < K) ? off : kOutOfRange;
+}
+
 // This wave's 8-row groups i0 .. i0+n-1 of a 256-row tile with 128-byte rows.
+template <bool kK128>
 __device__ __forceinline__ void dma_tile128(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows,
                                             int K, int k0, int wave, int lane, int i0 = 0,
                                             int n = kWideDmaPerWave) {
@@ -406,7 +418,7 @@ __device__ __forceinline__ void dma_tile128(__amdgpu_buffer_rsrc_t r, uint8_t* l
     const int group = wave * kWideDmaPerWave + i;  // 8 rows per instruction
     const int row = group * 8 + r8;
     const int gk = k0 + 16 * (p ^ swz128(row));
-    const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
+    const unsigned off = copy_offset<kK128>(row, rows, gk, K);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off,
         0, 0, 0);
@@ -427,8 +439,8 @@ __device__ __forceinline__ i32x8 frag128(const uint8_t* tile, int row, int fg, i
 }
 
 // kStore: 0 = 2-byte stores, 1 = 8-byte stores (N % 4 == 0), 2 = through LDS with
-// 16-byte row stores (N % 8 == 0, output 16-byte aligned).
-template <int kStore>
+// 16-byte row stores (N % 8 == 0, output 16-byte aligned).  kK128: K % 128 == 0 (copy_offset).
+template <int kStore, bool kK128 = false>
 __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
     const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
     float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
@@ -457,8 +469,12 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
   auto b_tile = [&](int step) { return smem + (3 + (step & 1)) * kWideOperandBytes; };
   // The wave index as a scalar: each copy's LDS destination (M0) is then scalar arithmetic.
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  auto copy_a = [&](int step, int g0, int n) { dma_tile128(xa, a_tile(step), rows_a, K, step * WBK, wave_s, lane, g0, n); };
-  auto copy_b = [&](int step, int g0, int n) { dma_tile128(wb, b_tile(step), rows_b, K, step * WBK, wave_s, lane, g0, n); };
+  auto copy_a = [&](int step, int g0, int n) {
+    dma_tile128<kK128>(xa, a_tile(step), rows_a, K, step * WBK, wave_s, lane, g0, n);
+  };
+  auto copy_b = [&](int step, int g0, int n) {
+    dma_tile128<kK128>(wb, b_tile(step), rows_b, K, step * WBK, wave_s, lane, g0, n);
+  };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * WM + fr, brow = wn * WN + fr;
 
@@ -567,16 +583,17 @@ constexpr int kHalfLaunchLdsBytes = kHalfLdsBytes + kBiasBytes;  // 144.5 KiB
 static_assert(kHalfCopies % 2 == 0, "each half step issues half the copies");
 
 // Group `group` (8 rows) of a tile with 128-byte rows: one direct-to-LDS instruction.
+template <bool kK128>
 __device__ __forceinline__ void dma_group128(__amdgpu_buffer_rsrc_t r, uint8_t* lds_tile, int rows, int K,
                                              int k0, int group, int lane) {
   const int row = group * 8 + lane / 8;
   const int gk = k0 + 16 * ((lane % 8) ^ swz128(row));
-  const unsigned off = (row < rows && gk < K) ? (unsigned)(row * K + gk) : kOutOfRange;
+  const unsigned off = copy_offset<kK128>(row, rows, gk, K);
   __builtin_amdgcn_raw_ptr_buffer_load_lds(
       r, (__attribute__((address_space(3))) void*)(lds_tile + group * kSlotsPerInst * 16), 16, off, 0, 0, 0);
 }
 
-template <int kStore>
+template <int kStore, bool kK128 = false>
 __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
     const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
     float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
@@ -606,9 +623,9 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_half(
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   auto copy = [&](int step, int c) {
     if (c < kHalfXDma)
-      dma_group128(xa, a_tile(step), rows_a, K, step * WBK, wave_s * kHalfXDma + c, lane);
+      dma_group128<kK128>(xa, a_tile(step), rows_a, K, step * WBK, wave_s * kHalfXDma + c, lane);
     else
-      dma_group128(wb, b_tile(step), rows_b, K, step * WBK, wave_s * kWideDmaPerWave + c - kHalfXDma, lane);
+      dma_group128<kK128>(wb, b_tile(step), rows_b, K, step * WBK, wave_s * kWideDmaPerWave + c - kHalfXDma, lane);
   };
   const int fr = lane % 32, fg = lane / 32;
   const int arow = wm * 32 * kHalfMI + fr, brow = wn * WN + fr;
