@@ -503,6 +503,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[i][j] = mfma32_e4m3(b0[j], a0[i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);  // the MFMA issues before its copy
         if (j % 2 == 1) copy_a(kt + 2, 2 * i + j / 2, 1);
         part[j] = j < 2 ? frag128_part(b_tile(kt), brow + 32 * i, fg, 1, j)
                         : frag128_part(a_tile(kt), arow + 32 * i, fg, 1, j - 2);
@@ -523,6 +524,7 @@ __global__ __launch_bounds__(kThreads) void fp8_gemm_wide(
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         acc[i][j] = mfma32_e4m3(b1[j], a1[i], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);  // the MFMA issues before its copy
         if (j % 2 == i % 2) copy_b(kt + 2, 2 * i + j / 2, 1);
         part[j] = j < 2 ? frag128_part(b_tile(kt + 1), brow + 32 * i, fg, 0, j)
                         : frag128_part(a_tile(kt + 1), arow + 32 * i, fg, 0, j - 2);
