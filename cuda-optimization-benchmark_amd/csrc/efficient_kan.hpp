@@ -148,7 +148,8 @@ __host__ __device__ inline double kan_row_spacing(const float (&kn)[kMaxKnots], 
 // recursion on the row's own knots (kan_table_entry) it differs by the row's deviation from
 // uniform, about 1e-6 of a basis value at most, the same approximation kan_fused makes when
 // it evaluates these pieces itself; it needs one division where the recursion needs 32.
-__host__ __device__ inline void kan_cardinal_entry(int L, int j, double h, float* __restrict__ dst) {
+// ent: the interval's 16 floats.
+__device__ __forceinline__ void kan_cardinal_entry(int L, int j, double h, float* ent) {
   constexpr double kPiece[4][4] = {{0.0, 0.0, 0.0, 1.0 / 6.0},
                                    {1.0 / 6.0, 0.5, 0.5, -0.5},
                                    {2.0 / 3.0, 0.0, -1.0, 0.5},
@@ -161,16 +162,15 @@ __host__ __device__ inline void kan_cardinal_entry(int L, int j, double h, float
     const bool exists = kb >= 0 && kb <= L - 2 - kOrder;
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-      dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] =
-          exists ? (float)(kPiece[kOrder - r][c] * ihp[c]) : 0.0f;
+      ent[4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = exists ? (float)(kPiece[kOrder - r][c] * ihp[c]) : 0.0f;
   }
 }
 
-// Entry j of a feature's table (dst: the feature's 16 * L floats): j = -1 writes the knot
-// row, j in [0, L-1) interval j's cubics.
-__host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, int L, int j, float* __restrict__ dst) {
+// Entry j of a feature's table (ent: the entry's 16 floats): j = -1 the knot row, j in
+// [0, L-1) interval j's cubics.
+__device__ __forceinline__ void kan_table_entry(const float* __restrict__ knots_row, int L, int j, float* ent) {
   if (j < 0) {
-    for (int k = 0; k < kMaxKnots; ++k) dst[k] = k < L ? knots_row[k] : __builtin_inff();
+    for (int k = 0; k < kMaxKnots; ++k) ent[k] = k < L ? knots_row[k] : __builtin_inff();
     return;
   }
   // The recursion for interval j only reads knots j-3 .. j+4; w[i] = t_{j-3+i} (0 outside the
@@ -219,7 +219,7 @@ __host__ __device__ void kan_table_entry(const float* __restrict__ knots_row, in
 #pragma unroll
   for (int r = 0; r <= kOrder; ++r)  // basis j - 3 + r; (j - 3 + r) % 4 == (j + 1 + r) % 4
 #pragma unroll
-    for (int c = 0; c < 4; ++c) dst[kMaxKnots + j * 16 + 4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
+    for (int c = 0; c < 4; ++c) ent[4 * tbl_chunk(j, (j + 1 + r) & 3) + c] = (float)P[r][c];
 }
 
 
@@ -256,35 +256,52 @@ __host__ __device__ constexpr int spline_basis(int s) {
   return kCp == 8 ? (s < 4 ? 2 * s : 2 * (s - 4) + 1) : 4 * (s % 4) + s / 4;
 }
 
-// Basis table entries first .. first + count - 1 (L per feature: the knot row and the L - 1
-// intervals), one per thread in turn.  Returns this thread's flags: bit 0 every knot row it
-// wrote is uniform to 1e-3 h, bit 1 to 5e-7 h (kan_knots_uniform); the caller combines them.
-__device__ __forceinline__ int kan_tables_range(int first, int count, const float* __restrict__ grid, int I,
-                                                int L, int ngroups, float* __restrict__ tables) {
+// Basis table entries first .. first + kPackThreads - 1 (L per feature: the knot row and
+// the L - 1 intervals, 64 bytes each), one per thread.  Each thread builds its entry in LDS;
+// then every thread stores 16-byte chunks of consecutive entries, so a wave's store covers
+// 1 KiB of the table (entries are consecutive in memory within a feature group).  Written
+// one float at a time from the thread that computed it, each store instruction touched 64
+// separate lines and the 24 table workgroups at BASELINE took about 6 us.  Returns this
+// thread's flags: bit 0 every knot row it wrote is uniform to 1e-3 h, bit 1 to 5e-7 h
+// (kan_knots_uniform); the caller combines them.
+constexpr int kTableThreads = 512;
+__device__ __forceinline__ int kan_tables_range(int first, const float* __restrict__ grid, int I, int L,
+                                                int ngroups, float* __restrict__ tables) {
+  __shared__ f32x4 stage[kTableThreads * 4];  // entry e at stage[4e .. 4e + 3]
   bool uniform = true, cardinal = true;
-  for (int e = (int)threadIdx.x; e < count; e += (int)blockDim.x) {
-    const int idx = first + e;
+  const int tid = (int)threadIdx.x;
+  const int nent = ngroups * kGroup * L;  // entries past it belong to no group
+  {
+    const int idx = first + tid;
     const int f = idx / L, j = idx % L - 1;
-    if (f >= ngroups * kGroup) break;
-    float* dst = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(tables) +
-                                          (size_t)(f / kGroup) * tbl_group_bytes(L) + (f % kGroup) * 64 * L);
-    if (f < I) {
+    float* ent = reinterpret_cast<float*>(stage + 4 * tid);
+    if (idx < nent && f < I) {
       float kn[kMaxKnots];
 #pragma unroll
       for (int k = 0; k < kMaxKnots; ++k) kn[k] = k < L ? grid[(size_t)f * L + k] : 0.0f;
       const bool row_cardinal = kan_knots_uniform(kn, L, kCardinalRel);
       if (j >= 0 && row_cardinal)
-        kan_cardinal_entry(L, j, kan_row_spacing(kn, L), dst);
+        kan_cardinal_entry(L, j, kan_row_spacing(kn, L), ent);
       else
-        kan_table_entry(grid + (size_t)f * L, L, j, dst);
+        kan_table_entry(grid + (size_t)f * L, L, j, ent);
       if (j < 0) {
         uniform = uniform && kan_knots_uniform(kn, L, kUniformRel);
         cardinal = cardinal && row_cardinal;
       }
-    } else if (j < 0) {  // missing feature: knots 0, 1, 2, ... and zero coefficients
-      for (int k = 0; k < kMaxKnots; ++k) dst[k] = (float)k;
-    } else {
-      for (int k = 0; k < 16; ++k) dst[kMaxKnots + 16 * j + k] = 0.0f;
+    } else if (idx < nent) {  // missing feature: knots 0, 1, 2, ... and zero coefficients
+      for (int k = 0; k < 16; ++k) ent[k] = j < 0 ? (float)k : 0.0f;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int c = tid + kTableThreads * i;  // chunk c % 4 of entry c / 4
+    const int idx = first + c / 4;
+    if (idx < nent) {
+      const int f = idx / L, e = idx % L;
+      uint8_t* dst = reinterpret_cast<uint8_t*>(tables) + (size_t)(f / kGroup) * tbl_group_bytes(L) +
+                     ((f % kGroup) * L + e) * 64 + 16 * (c % 4);
+      *reinterpret_cast<f32x4*>(dst) = stage[c];
     }
   }
   return (uniform ? 1 : 0) | (cardinal ? 2 : 0);
@@ -312,6 +329,7 @@ __device__ __forceinline__ int kan_tables_range(int first, int count, const floa
 constexpr int kPackCols = 2;
 constexpr int kColWaves = 4;
 constexpr int kPackThreads = kPackCols * kColWaves * kWave;
+static_assert(kPackThreads == kTableThreads, "a table workgroup is one kan_pack workgroup");
 // Workgroup t's pair of output columns (pass 1 and pass 2 above).
 template <int kCp, bool kVecW>
 __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb, const float* __restrict__ ws,
@@ -500,7 +518,7 @@ __global__ __launch_bounds__(kPackThreads) __attribute__((amdgpu_waves_per_eu(4)
   const int t = (int)blockIdx.x - tblocks;
   if (t < 0) {
     const int b = (int)blockIdx.x;
-    const int flags = kan_tables_range(b * kPackThreads, kPackThreads, grid, I, L, ngroups, tables);
+    const int flags = kan_tables_range(b * kTableThreads, grid, I, L, ngroups, tables);
     const bool uniform = __syncthreads_and(flags & 1), cardinal = __syncthreads_and(flags & 2);
     if (threadIdx.x == 0) uflags[b] = (uniform ? 1 : 0) | (cardinal ? 2 : 0);
     return;
