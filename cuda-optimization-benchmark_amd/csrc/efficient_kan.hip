@@ -62,13 +62,13 @@ __global__ __launch_bounds__(kRowThreads) void kan_rowwise(
 }
 
 // True when every 32-bit buffer offset of the fast path fits: x, out, the prepared weights
-// and one output column's row of Ws (kan_pack's descriptors start at their column) each
-// under 2 GiB.  Ws as a whole may be larger.
+// and one column pair's rows of Ws (kan_pack's descriptors start at their pair) each under
+// 2 GiB.  Ws as a whole may be larger.
 bool fast_path_fits(int B, int I, int O, int Cp) {
   using namespace kan;
   const size_t ngroups = (I + kGroup - 1) / kGroup, Opad = ((O + BN - 1) / BN) * (size_t)BN;
   const size_t lim = 0x7fffffffu;
-  return (size_t)B * I * 4 < lim && (size_t)B * O * 4 < lim && (size_t)I * Cp * 4 < lim &&
+  return (size_t)B * I * 4 < lim && (size_t)B * O * 4 < lim && (size_t)kPackCols * I * Cp * 4 < lim &&
          ngroups * (1 + Cp) * Opad * kChunk * 2 < lim;
 }
 

@@ -309,17 +309,23 @@ __device__ __forceinline__ int kan_tables_range(int first, const float* __restri
 
 // kan_pack: the first tblocks workgroups build the basis tables, kPackThreads entries each
 // (kan_tables_range), and write one knot-row flag word each; they need nothing from the
-// packing, so they run beside it.  Workgroup tblocks + t owns output columns kPackCols*t ..
-// +kPackCols-1 with kColWaves waves each (pack_columns); wave q of a column takes the runs
-// of 64 features q*64 + 64*kColWaves*j (lane = feature within the run), so a wave's loads
-// cover 64 consecutive features of the column's contiguous rows.  Pass 1 reduces the
-// column's max |w| over Wb, sc and Ws to colscale[o] (waves combine through LDS); pass 2
-// reads the column again (now from the L2 or the Infinity Cache) and writes its hi/lo
-// weights: lane (column o, feature f) writes all of f's bases, one run of Cp slots at
-// spline_k(f % 32) in the permuted basis order, and lanes with f % 32 < 4 also write silu
-// slots 8 (f % 32) .. +7.  Workgroup tblocks also zeroes kan_fused's split-K arrival
-// counters (their place in the workspace moves with the shape, so every call starts them
-// from zero).
+// packing, so they run beside it.  Workgroup tblocks + t owns the column pair 2t, 2t + 1
+// (pack_columns) with all 8 waves: lanes 0-31 of a wave take column 2t and lanes 32-63
+// column 2t + 1, lane fl of a half feature fl of a group (32 features).  Each wave takes
+// pack_runs runs of a batch (4 for Cp = 8, 1 for Cp = 16): wave w takes groups w, w + 8,
+// w + 16, ... of the batch, so a run's loads cover 1 KiB (Cp = 8) of one column's
+// contiguous Ws rows per half-wave.  Pass 1 reduces each column's max |w| over Wb, sc and Ws to
+// colscale[o] (the waves combine through LDS); pass 2 writes the hi/lo weights: lane
+// (column o, feature f) writes all of f's bases, one run of Cp slots at spline_k(f % 32) in
+// the permuted basis order, and lanes with f % 32 < 4 also write silu slots 8 (f % 32) .. +7.
+// The pair's two 64-byte halves of a chunk make one 128-byte line and both come from one
+// store instruction, so every store writes whole lines.  With one column per wave (each
+// line's halves written by two waves) the same data movement took 23.5 us against 18.4 us
+// (a `_work` probe of this phase alone).  When one batch covers every feature (I <= 1024 for
+// Cp = 8, I <= 256 for Cp = 16) it stays in registers between the passes; wider inputs read
+// each run again in pass 2 (from the L2 or the Infinity Cache).  Workgroup tblocks also
+// zeroes kan_fused's split-K arrival counters (their place in the workspace moves with the
+// shape, so every call starts them from zero).
 // At BASELINE the columns are 512 workgroups, as many as are resident at once, and the 24
 // table workgroups hold slots until they finish, so table time delays the last column
 // workgroups.  Measured (one box, median of 150): 15.6 us without tables, 21.7 us with
@@ -327,10 +333,17 @@ __device__ __forceinline__ int kan_tables_range(int first, const float* __restri
 // closed form for cardinal rows as well; building the tables inside the column workgroups,
 // before or after their columns, measured 23.7-26.7 us.
 constexpr int kPackCols = 2;
-constexpr int kColWaves = 4;
-constexpr int kPackThreads = kPackCols * kColWaves * kWave;
+constexpr int kPackWaves = 8;
+constexpr int kPackThreads = kPackWaves * kWave;
+// Runs per wave and batch (a batch is kPackWaves * runs groups): 4 for Cp = 8 and 1 for
+// Cp = 16, which keeps a batch's rows within the 128 registers of four waves per SIMD.
+// With 2 runs for Cp = 16 the reference's timed shape (I = 256, one group per wave) took
+// 78.0-78.2 us per call against 74.6-75.9 us with 1 run (A/B on one box, both orders).
+template <int kCp>
+constexpr int pack_runs() { return kCp == 8 ? 4 : 1; }
 static_assert(kPackThreads == kTableThreads, "a table workgroup is one kan_pack workgroup");
-// Workgroup t's pair of output columns (pass 1 and pass 2 above).
+static_assert(kPackCols * kGroup == kWave, "a wave's halves are the pair's two columns");
+// Workgroup t's column pair (pass 1 and pass 2 above).
 template <int kCp, bool kVecW>
 __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb, const float* __restrict__ ws,
                                              const float* __restrict__ sc, int I, int O, int C, int Opad,
@@ -338,102 +351,89 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
                                              _Float16* __restrict__ blo, int ngroups, unsigned* __restrict__ counters,
                                              int ncounters) {
   static_assert(kCp % 8 == 0, "whole 8-slot runs");
-  __shared__ float colmax[kPackCols][kColWaves];
+  __shared__ float colmax[kPackCols][kPackWaves];
   constexpr int kSub = 1 + kCp;
-  constexpr int kStride = kColWaves * kWave;  // features between a wave's runs
+  constexpr int kPackRuns = pack_runs<kCp>();
+  constexpr int kPackBatch = kPackWaves * kPackRuns;
   if (t == 0)
     for (int i = threadIdx.x; i < ncounters; i += kPackThreads) counters[i] = 0u;
   const int lane = (int)threadIdx.x % kWave, wave = (int)threadIdx.x / kWave;
-  const int oc = wave / kColWaves, q = wave % kColWaves;
-  const int o = t * kPackCols + oc;
-  const int first = q * kWave + lane;
+  const int oc = lane / kGroup, fl = lane % kGroup;
+  const int o0 = t * kPackCols, o = o0 + oc;
   const bool col = o < O;
-  constexpr bool vec = kVecW;  // C % 4 == 0 and ws 16-byte aligned: 16-byte row loads
-  const float* wsc = ws + (size_t)o * I * C;
-  // Ws[o, f, c] for c < kCp (zero past C), times s.
-  auto spline_row = [&](int f, float s, float (&v)[kCp]) {
-    const float* row = wsc + (size_t)f * C;
-    if constexpr (vec) {
+
+  // Pass 1: max over each column.  max_c |ws * s| = |s| * max_c |ws| exactly (rounding is
+  // monotonic).  Every load of a batch is a buffer load with no branch around it (an offset
+  // past the buffer reads zero for a missing feature, column or basis), so all of them are
+  // in flight before the first is used: behind per-run branches the compiler waited for
+  // each run's loads before issuing the next run's, one memory round trip per run.
+  // The descriptors start at the pair's first column and cover its columns below O, so
+  // their 32-bit offsets need only two columns' rows to fit (Ws as a whole may pass 2 GiB);
+  // a pair past O reads nothing.
+  const int ncols = O - o0 >= kPackCols ? kPackCols : (O > o0 ? O - o0 : 0);
+  const size_t obase = ncols > 0 ? (size_t)o0 : 0;
+  const __amdgpu_buffer_rsrc_t rwb = make_rsrc(wb + obase * I, (size_t)ncols * I * 4);
+  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc + obase * I, (size_t)ncols * I * 4);
+  const __amdgpu_buffer_rsrc_t rws = make_rsrc(ws + obase * I * C, (size_t)ncols * I * C * 4);
+  const unsigned cwb = (unsigned)oc * (unsigned)I * 4u;               // this lane's column in rwb, rsc
+  const unsigned cws = (unsigned)oc * (unsigned)I * (unsigned)C * 4u;  // and in rws
+  float wbv[kPackRuns], scv[kPackRuns], rows[kPackRuns][kCp];
+  // Run u of batch bt is group bt * kPackBatch + u * kPackWaves + wave; its loads go into
+  // wbv[u], scv[u] and rows[u].
+  auto load_run = [&](int bt, int u) {
+    const int f = (bt * kPackBatch + u * kPackWaves + wave) * kGroup + fl;
+    const bool ok = col && f < I;
+    const unsigned off = ok ? cwb + (unsigned)f * 4u : kOutOfRange;
+    wbv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rwb, off, 0, 0));
+    scv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, off, 0, 0));
+    const unsigned row = cws + (unsigned)f * (unsigned)C * 4u;
+    if constexpr (kVecW) {  // C % 4 == 0 and ws 16-byte aligned: 16-byte row loads
 #pragma unroll
       for (int c4 = 0; c4 < kCp / 4; ++c4) {
-        f32x4 w4 = {0.f, 0.f, 0.f, 0.f};
-        if (4 * c4 < C) w4 = *reinterpret_cast<const f32x4*>(row + 4 * c4);
+        const unsigned o4 = ok && 4 * c4 < C ? row + 16u * c4 : kOutOfRange;
+        const f32x4 w4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rws, o4, 0, 0));
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[4 * c4 + e] = w4[e] * s;
+        for (int e = 0; e < 4; ++e) rows[u][4 * c4 + e] = w4[e];
       }
     } else {
 #pragma unroll
-      for (int c = 0; c < kCp; ++c) v[c] = c < C ? row[c] * s : 0.0f;
-    }
-  };
-
-  // Pass 1: max over the column.  max_c |ws * s| = |s| * max_c |ws| exactly (rounding is
-  // monotonic).  A wave's runs go four at a time, and every load of a batch is a buffer
-  // load with no branch around it (an offset past the buffer reads zero for a missing
-  // feature, column or basis), so all of them are in flight before the first is used:
-  // behind per-run branches the compiler waited for each run's loads before issuing the
-  // next run's, one memory round trip per run.  The last four runs stay in registers for
-  // pass 2.
-  // The descriptors start at this wave's column, so their 32-bit offsets cover any I (Ws as
-  // a whole may pass 2 GiB).  A column past O reads nothing (every offset out of range).
-  const size_t ocol = col ? (size_t)o : 0;
-  const __amdgpu_buffer_rsrc_t rwb = make_rsrc(wb + ocol * I, (size_t)I * 4);
-  const __amdgpu_buffer_rsrc_t rsc = make_rsrc(sc + ocol * I, (size_t)I * 4);
-  const __amdgpu_buffer_rsrc_t rws = make_rsrc(ws + ocol * I * C, (size_t)I * C * 4);
-  float mx = 0.0f;
-  float wbv[4], scv[4], rows[4][kCp];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {  // a lane with no feature below I writes zeros in pass 2
-    wbv[u] = 0.0f;
-    scv[u] = 0.0f;
-#pragma unroll
-    for (int c = 0; c < kCp; ++c) rows[u][c] = 0.0f;
-  }
-  for (int f0 = first; f0 < I; f0 += 4 * kStride) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int f = f0 + u * kStride;
-      const bool ok = col && f < I;
-      const unsigned off = ok ? (unsigned)f * 4u : kOutOfRange;
-      wbv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rwb, off, 0, 0));
-      scv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsc, off, 0, 0));
-      const unsigned row = (unsigned)f * (unsigned)C * 4u;
-      if constexpr (vec) {
-#pragma unroll
-        for (int c4 = 0; c4 < kCp / 4; ++c4) {
-          const unsigned o4 = ok && 4 * c4 < C ? row + 16u * c4 : kOutOfRange;
-          const f32x4 w4 = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rws, o4, 0, 0));
-#pragma unroll
-          for (int e = 0; e < 4; ++e) rows[u][4 * c4 + e] = w4[e];
-        }
-      } else {
-#pragma unroll
-        for (int c = 0; c < kCp; ++c) {
-          const unsigned o1 = ok && c < C ? row + 4u * c : kOutOfRange;
-          rows[u][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rws, o1, 0, 0));
-        }
+      for (int c = 0; c < kCp; ++c) {
+        const unsigned o1 = ok && c < C ? row + 4u * c : kOutOfRange;
+        rows[u][c] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rws, o1, 0, 0));
       }
     }
+  };
+  auto load_batch = [&](int bt) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kPackRuns; ++u) load_run(bt, u);
+  };
+  const int nbatch = (ngroups + kPackBatch - 1) / kPackBatch;
+  float mx = 0.0f;
+#pragma unroll 1
+  for (int bt = 0; bt < nbatch; ++bt) {
+    load_batch(bt);
+#pragma unroll
+    for (int u = 0; u < kPackRuns; ++u) {
       float m = 0.0f;
 #pragma unroll
       for (int c = 0; c < kCp; ++c) m = fmaxf(m, fabsf(rows[u][c]));
       mx = fmaxf(mx, fmaxf(fabsf(wbv[u]), fabsf(scv[u]) * m));
     }
   }
-  for (int off = kWave / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
-  if (lane == 0) colmax[oc][q] = mx;
+  for (int off = kGroup / 2; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));  // within a half
+  if (fl == 0) colmax[oc][wave] = mx;
   __syncthreads();
 #pragma unroll
-  for (int w = 0; w < kColWaves; ++w) mx = fmaxf(mx, colmax[oc][w]);
+  for (int w = 0; w < kPackWaves; ++w) mx = fmaxf(mx, colmax[oc][w]);
   int e = 0;
   if (mx > 0.0f && mx < __builtin_inff()) e = 14 - ilogbf(mx);
   e = e > 100 ? 100 : (e < -100 ? -100 : e);
-  if (q == 0 && lane == 0) colscale[o] = ldexpf(1.0f, -e);
+  if (wave == 0 && fl == 0) colscale[o] = ldexpf(1.0f, -e);
   const float scale = ldexpf(1.0f, e);  // 2^e, exact
 
-  // Pass 2: the scaled hi/lo weights of every group (zero past I and O).
+  // Pass 2: the scaled hi/lo weights of every group (zero past I and O).  The pair's two
+  // columns of a chunk are one 128-byte line, and a wave writes both halves, so each store
+  // instruction writes whole lines.
   auto put = [&](int g, int sub, int slot, const float* v) {
     f16x8 h8, l8;
 #pragma unroll
@@ -449,7 +449,7 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
   };
   // Feature fl's bases in the GEMM's sparse K order (spline_k): one run of C' slots, the
   // bases permuted so every group of 4 slots holds at most two of the four nonzero ones.
-  auto put_spline = [&](int g, int fl, const float (&v)[kCp]) {
+  auto put_spline = [&](int g, const float (&v)[kCp]) {
     int sub, slot;
     spline_k<kCp>(fl, sub, slot);
     float w[kCp];
@@ -458,52 +458,33 @@ __device__ __forceinline__ void pack_columns(int t, const float* __restrict__ wb
 #pragma unroll
     for (int h = 0; h < kCp / 8; ++h) put(g, sub, slot + 8 * h, w + 8 * h);
   };
-  if (ngroups * kGroup <= 4 * kStride) {
-    // One batch of runs covers every feature (I <= 1024): pass 1's registers hold the
-    // column's data.  Lane f % 32 < 4 of a group takes the silu weights of features
-    // 8 (f % 32) .. +7 from the lanes that loaded them (a group sits within one run).
+  // Lane fl < 4 of a half takes the silu weights of features 8 fl .. +7 of its group from
+  // the lanes that loaded them.
+  auto write_run = [&](int bt, int u) {
+    const int g = bt * kPackBatch + u * kPackWaves + wave;
+    float v[kCp], silu[8];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int f = first + u * kStride, g = f / kGroup, fl = f % kGroup;
-      float v[kCp], silu[8];
+    for (int c = 0; c < kCp; ++c) v[c] = rows[u][c] * scv[u];
 #pragma unroll
-      for (int c = 0; c < kCp; ++c) v[c] = rows[u][c] * scv[u];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) silu[k] = __shfl(wbv[u], (lane & 32) + ((8 * (lane & 3) + k) & 31), kWave);
-      if (f < ngroups * kGroup) {
-        put_spline(g, fl, v);
-        if (fl < 4) put(g, 0, 8 * fl, silu);
-      }
+    for (int k = 0; k < 8; ++k) silu[k] = __shfl(wbv[u], (lane & kGroup) + ((8 * (lane & 3) + k) & (kGroup - 1)), kWave);
+    if (g < ngroups) {
+      put_spline(g, v);
+      if (fl < 4) put(g, 0, 8 * fl, silu);
     }
+  };
+  if (nbatch == 1) {  // pass 1's registers hold the column pair's data
+#pragma unroll
+    for (int u = 0; u < kPackRuns; ++u) write_run(0, u);
     return;
   }
-  for (int f0 = first; f0 < ngroups * kGroup; f0 += 2 * kStride) {
-    float rows2[2][kCp], silu[2][8];
+  // Wider inputs: each run again, loaded and written in turn (one run's registers live).
+#pragma unroll 1
+  for (int bt = 0; bt < nbatch; ++bt)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = f0 + u * kStride, g = f / kGroup, fl = f % kGroup;
-#pragma unroll
-      for (int c = 0; c < kCp; ++c) rows2[u][c] = 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) silu[u][k] = 0.0f;
-      if (col && f < I) spline_row(f, sc[(size_t)o * I + f], rows2[u]);
-      if (fl < 4) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const int f2 = g * kGroup + 8 * fl + k;
-          if (col && f2 < I) silu[u][k] = wb[(size_t)o * I + f2];
-        }
-      }
+    for (int u = 0; u < kPackRuns; ++u) {
+      load_run(bt, u);
+      write_run(bt, u);
     }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int f = f0 + u * kStride, g = f / kGroup, fl = f % kGroup;
-      if (f < ngroups * kGroup) {
-        put_spline(g, fl, rows2[u]);
-        if (fl < 4) put(g, 0, 8 * fl, silu[u]);
-      }
-    }
-  }
 }
 
 // Four waves per SIMD (at most 128 VGPRs): two workgroups per CU, so 512 column workgroups

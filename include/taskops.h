@@ -114,7 +114,7 @@ hipError_t taskops_ppo_clip_entropy_noalloc(int32_t B, int32_t T, int32_t H,
  * in magnitude (smaller ones lose bits to the fp16 low halves); knot rows uniform to
  * 5e-7 h use the cardinal cubic pieces (about 1e-6 of a basis value from the exact bases),
  * all other rows exact per-interval cubics.  It also needs x, out, its packed weights and
- * one output column's I x 16 spline slots each under 2 GiB (spline_weight as a whole may be
+ * two output columns' I x 16 spline slots each under 2 GiB (spline_weight as a whole may be
  * larger).  Other orders, knot counts and sizes take an fp32 row-wise path without these
  * limits.
  * Replaces: reference/efficient_kan/solution.cu:177-288
