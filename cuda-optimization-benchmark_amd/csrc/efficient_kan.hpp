@@ -1157,7 +1157,9 @@ __device__ __forceinline__ void store_slot(f32x4 val, int wq, int rb, int cb, in
 // releases them at agent scope and arrives on the tile's counter; the tile's last arrival
 // sums the nsplit partials of every slot in split order (so the result does not depend on
 // which split arrives last), 16 slots per thread with each split's loads in flight
-// together, resets the counter and writes the output.
+// together, resets the counter and writes the output.  (Giving each wave 16 consecutive
+// slot rows, so both 64-byte halves of an output line leave from one wave, measured about
+// 1 us slower per call at the reference's timed shape.)
 __device__ __forceinline__ void split_k_finish(uint8_t* smem, int tid, int split, int nsplit, int tile, int m0,
                                                int n0, int B, int O, const float* __restrict__ colscale,
                                                float* __restrict__ out, const float* __restrict__ partial,
@@ -1287,12 +1289,26 @@ __global__ __launch_bounds__(kThreads) void kan_fused(
     return;
   }
 
-  // Epilogue.
+  // Epilogue.  Each accumulator holds one column of 4 rows, so a store instruction writes
+  // 64-byte halves of 4 output lines; the wave's four column blocks of a row go out back to
+  // back, so both halves of each line leave in consecutive instructions.  Same bits; A/B on
+  // one box (BASELINE): 258.3 against 260.4 us per call with the column blocks outermost.
+  // Staging each row block in LDS to store 256-byte row segments measured the same (258.2).
   const __amdgpu_buffer_rsrc_t ro = make_rsrc(out, (size_t)B * O * 4);
+  const int fr = lane % 16, fq = lane / 16;
+  float csc[kCB];
 #pragma unroll
-  for (int cb = 0; cb < kCB; ++cb)
+  for (int cb = 0; cb < kCB; ++cb) csc[cb] = colscale[n0 + wave * (kCB * 16) + cb * 16 + fr];
 #pragma unroll
-    for (int rb = 0; rb < kRB; ++rb) store_slot(acc[rb][cb], wave, rb, cb, lane, m0, n0, B, O, colscale, ro);
+  for (int rb = 0; rb < kRB; ++rb)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int cb = 0; cb < kCB; ++cb) {
+        const int row = m0 + rb * 16 + 4 * fq + e, o = n0 + wave * (kCB * 16) + cb * 16 + fr;
+        const unsigned off = (row < B && o < O) ? (unsigned)(((size_t)row * O + o) * 4) : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[rb][cb][e] * csc[cb]), ro, off, 0, 0);
+      }
 }
 
 }  // namespace kan
