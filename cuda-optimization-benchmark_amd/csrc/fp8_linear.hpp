@@ -708,13 +708,24 @@ constexpr int kSkinnyWaves = 8;
 constexpr int kSkinnyThreads = kSkinnyWaves * kWave;
 constexpr int kSkinnyMaxM = 64;
 
+// Column block of workgroup b among nb: a bf16 output line (64 columns) is four 16-column
+// blocks, and workgroups are dispatched round-robin over the 8 XCDs, so XCD x's workgroups
+// b = x + 8 j take whole lines, 4 (x + 8 (j / 4)) + j % 4, and a line's four partial writes
+// merge in one L2 (a bijection on the first 32 floor(nb / 32) blocks; the rest keep their
+// index).  Dispatch order only affects speed, never which outputs are written.
+__device__ __forceinline__ int skinny_block(int b, int nb) {
+  if (b >= nb / 32 * 32) return b;
+  const int x = b % 8, j = b / 8;
+  return 4 * (x + 8 * (j / 4)) + j % 4;
+}
+
 template <int kVec>
 __global__ __launch_bounds__(kSkinnyThreads) void fp8_gemm_skinny(
     const uint8_t* __restrict__ x, const uint8_t* __restrict__ w, int M, int N, int K,
     float inv_scale, const uint16_t* __restrict__ bias, uint16_t* __restrict__ out) {
   __shared__ float part[kSkinnyWaves][kSkinnyMaxM][16];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = skinny_block(blockIdx.x, gridDim.x) * 16;
   const int fr = lane % 16, fg = lane / 16;
   const int rblocks = (M + 15) / 16;
   const int steps = (K + 127) / 128;
@@ -777,17 +788,6 @@ __global__ __launch_bounds__(kSkinnyThreads) void fp8_gemm_skinny(
 constexpr int skinny_slice(int rb) { return rb == 1 ? 512 : rb <= 3 ? 256 : 128; }
 constexpr int skinny_lds_bytes(int rb) {
   return kSkinnyWaves * (16 + 16 * rb) * skinny_slice(rb) + kSkinnyWaves * 16 * rb * 16 * 4;
-}
-
-// Column block of workgroup b among nb: a bf16 output line (64 columns) is four 16-column
-// blocks, and workgroups are dispatched round-robin over the 8 XCDs, so XCD x's workgroups
-// b = x + 8 j take whole lines, 4 (x + 8 (j / 4)) + j % 4, and a line's four partial writes
-// merge in one L2 (a bijection on the first 32 floor(nb / 32) blocks; the rest keep their
-// index).  Dispatch order only affects speed, never which outputs are written.
-__device__ __forceinline__ int skinny_block(int b, int nb) {
-  if (b >= nb / 32 * 32) return b;
-  const int x = b % 8, j = b / 8;
-  return 4 * (x + 8 * (j / 4)) + j % 4;
 }
 
 template <int kRB>  // row blocks of 16: M <= 16 * kRB
