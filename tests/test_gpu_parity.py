@@ -243,8 +243,12 @@ FP8_SHAPES = [
     (33, 48, 20, 0),
     (1, 16, 1, 0),
     (49, 400, 130, 0),
+    # more than 32 column blocks, not a multiple of 32 (63 and 38): the XCD-aware block order
+    # covers the first 32 and the rest keep their index
+    (16, 512, 1000, 0),
     # skinny with K % 16 != 0 (the register path)
     (5, 40, 7, 0),
+    (9, 40, 600, 0),
 ]
 
 
