@@ -161,29 +161,46 @@ MI355X_SIMDS = 256 * 4
 MI355X_XCDS = 8
 
 
+def dispatch_durations(d: str) -> dict:
+    """kernel name -> per-dispatch durations in ns, in dispatch order (the same dispatches
+    counter_values returns)."""
+    agg = collections.defaultdict(list)
+    for name, _, dur in sorted(_db(d).execute("select name, dispatch_id, duration from kernels"),
+                               key=lambda r: r[1]):
+        agg[name].append(float(dur))
+    return agg
+
+
 def mfma_util(d: str, simds: int = MI355X_SIMDS, xcds: int = MI355X_XCDS) -> dict:
-    """kernel -> {dispatches, busy_pct, f16_flop, f8_flop} (means over dispatches)."""
+    """kernel -> {dispatches, busy_pct, f16_flop, f8_flop, clock_ghz} (means over dispatches).
+    clock_ghz is GRBM_GUI_ACTIVE's cycles per XCD over the dispatch's duration: the shader
+    clock the kernel ran at (the peaks are quoted at 2.4 GHz)."""
     busy = counter_values(d, "SQ_VALU_MFMA_BUSY_CYCLES")
     gui = {k: [v / xcds for v in vs] for k, vs in counter_values(d, "GRBM_GUI_ACTIVE").items()}
     f16 = counter_values(d, "SQ_INSTS_VALU_MFMA_MOPS_F16")
     f8 = counter_values(d, "SQ_INSTS_VALU_MFMA_MOPS_F8")
+    durs = dispatch_durations(d)
     out = {}
     for k, b in busy.items():
         g = gui.get(k)
         if not g or sum(b) == 0:
             continue
+        t = durs.get(k, [])
+        clock = statistics.mean(gg / tt for gg, tt in zip(g, t) if tt > 0) if len(t) == len(g) else float("nan")
         out[k] = {"dispatches": len(b),
                   "busy_pct": 100.0 * statistics.mean(bb / (gg * simds) for bb, gg in zip(b, g)),
                   "f16_flop": 512.0 * statistics.mean(f16.get(k, [0.0])),
-                  "f8_flop": 512.0 * statistics.mean(f8.get(k, [0.0]))}
+                  "f8_flop": 512.0 * statistics.mean(f8.get(k, [0.0])),
+                  "clock_ghz": clock}
     return out
 
 
 def print_mfma(u: dict) -> None:
-    print("| kernel | dispatches | MFMA busy % | fp16 MFMA FLOP / dispatch | fp8 MFMA FLOP / dispatch |")
-    print("|---|---:|---:|---:|---:|")
+    print("| kernel | dispatches | MFMA busy % | clock GHz | fp16 MFMA FLOP / dispatch | fp8 MFMA FLOP / dispatch |")
+    print("|---|---:|---:|---:|---:|---:|")
     for k, r in sorted(u.items(), key=lambda kv: -kv[1]["busy_pct"]):
-        print(f"| `{_short(k)}` | {r['dispatches']} | {r['busy_pct']:.1f} | {r['f16_flop']:.4g} | {r['f8_flop']:.4g} |")
+        print(f"| `{_short(k)}` | {r['dispatches']} | {r['busy_pct']:.1f} | {r['clock_ghz']:.2f} | "
+              f"{r['f16_flop']:.4g} | {r['f8_flop']:.4g} |")
 
 
 def _write_json(path: str, body: dict, a) -> None:
