@@ -119,13 +119,16 @@ __device__ __forceinline__ float scale_from(unsigned m) {
   return (float)(448.0 / den);
 }
 
-// Codes of this thread's part of the chunk at `base` (q 4-byte aligned).
+// Codes of this thread's part of the chunk at `base` (q 4-byte aligned).  A whole chunk's
+// stores are non-temporal (each instruction writes 256 contiguous bytes, whole lines), so
+// the codes do not sit dirty in the L2s for the end of the kernel to write back: 19.5-19.6
+// -> 17.6-17.7 us per call at 4096 x 4096 (A/B on one box, both orders, same bits).
 __device__ __forceinline__ void store_chunk(uint8_t* __restrict__ q, int64_t n, int64_t base,
                                             const f32x4 (&v)[kVecs], float scale) {
   if (base + kChunk <= n) {
     unsigned* out = reinterpret_cast<unsigned*>(q + base) + threadIdx.x;
 #pragma unroll
-    for (int k = 0; k < kVecs; ++k) out[k * kThreads] = cvt4(v[k], scale);
+    for (int k = 0; k < kVecs; ++k) __builtin_nontemporal_store(cvt4(v[k], scale), out + k * kThreads);
     return;
   }
 #pragma unroll
