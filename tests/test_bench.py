@@ -143,3 +143,33 @@ def test_profiling_counters_table(tmp_path, capsys):
     assert profiling.main(["counters", str(tmp_path), "SQ_X", "--kernel", "fp8_gemm"]) == 0
     lines = [l for l in capsys.readouterr().out.splitlines() if l.startswith("| SQ_")]
     assert lines == ["| SQ_X | `fp8_gemm_half<2>` | 2 | 9 |"]
+
+
+def test_profiling_mfma_table_clock(tmp_path, capsys):
+    """profiling.py mfma: busy % = MFMA busy cycles over (GRBM_GUI_ACTIVE per XCD x SIMDs), and
+    the clock = GRBM_GUI_ACTIVE per XCD over the same dispatch's duration.  Two dispatches,
+    2000 cycles in 1000 ns (2 GHz) at 50 % busy and 3000 cycles in 2000 ns (1.5 GHz) at 25 %,
+    the counter summed over the 8 XCDs' instances."""
+    import sqlite3
+    from cob_amd import profiling
+    db = sqlite3.connect(tmp_path / "m_results.db")
+    db.execute("create table counters_collection (kernel_name text, dispatch_id int, counter_name text, value real)")
+    db.execute("create table kernels (name text, dispatch_id int, duration real)")
+    k, simds = "kan_fused<8>", profiling.MI355X_SIMDS
+    rows = []
+    for disp, cycles, busy in ((1, 2000.0, 0.5), (2, 3000.0, 0.25)):
+        rows += [(k, disp, "GRBM_GUI_ACTIVE", cycles)] * profiling.MI355X_XCDS
+        rows.append((k, disp, "SQ_VALU_MFMA_BUSY_CYCLES", busy * cycles * simds))
+        rows.append((k, disp, "SQ_INSTS_VALU_MFMA_MOPS_F16", 10.0))
+    db.executemany("insert into counters_collection values (?, ?, ?, ?)", rows)
+    db.executemany("insert into kernels values (?, ?, ?)", [(k, 1, 1000.0), (k, 2, 2000.0)])
+    db.commit()
+    db.close()
+    u = profiling.mfma_util(str(tmp_path))
+    assert set(u) == {k}
+    assert abs(u[k]["busy_pct"] - 37.5) < 1e-9
+    assert abs(u[k]["clock_ghz"] - 1.75) < 1e-9
+    assert u[k]["f16_flop"] == 512.0 * 10.0 and u[k]["dispatches"] == 2
+    profiling.print_mfma(u)
+    line = [l for l in capsys.readouterr().out.splitlines() if l.startswith("| `kan")][0]
+    assert line == "| `kan_fused<8>` | 2 | 37.5 | 1.75 | 5120 | 0 |"
