@@ -15,12 +15,14 @@
 // writes one partial max per workgroup; qz_cast reduces those partials (a few KiB from L2),
 // derives the scale and converts, reading x a second time.
 //
-// The kernels walk x in chunks of 16384 elements per workgroup and step.  A thread
-// issues all 16 of its 16-byte loads of a chunk before it uses any (64 floats in
-// registers), so each wave keeps 16 KiB in flight: at one chunk per workgroup, which a
+// The kernels walk x in chunks of 16384 elements per 512-thread workgroup and step.  A
+// thread issues all 8 of its 16-byte loads of a chunk before it uses any (32 floats in
+// registers), so each wave keeps 8 KiB in flight: at one chunk per workgroup, which a
 // 4096 x 4096 operand is on 256 CUs, a kernel is one round trip of loads.  Element
-// base + 4 * (k * 256 + t) + c of a chunk belongs to thread t, so every load and store
-// instruction of a wave covers contiguous memory.
+// base + 4 * (k * 512 + t) + c of a chunk belongs to thread t, so every load and store
+// instruction of a wave covers contiguous memory.  The same chunk as 256 threads x 16
+// loads was 17.83-17.84 us per fused call against 17.58-17.61 (A/B on two boxes, same
+// bits); 512 x 16 and 1024 x 8 were in between, 1024 x 16 slower (22.4).
 //
 // One launch (qz_fused, when the grid fits the resident capacity): each workgroup keeps its
 // chunk in registers, the workgroups combine their maxima through a grid barrier, and each
@@ -35,8 +37,8 @@
 namespace taskops {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kVecs = 16;                                       // f32x4 per thread per chunk
+constexpr int kThreads = 512;
+constexpr int kVecs = 8;                                        // f32x4 per thread per chunk
 constexpr int64_t kChunk = (int64_t)kThreads * kVecs * 4;        // elements per chunk
 constexpr int kPerThread = 16;  // elements per thread per step of the unaligned kernels
 constexpr int kMaxPartials = 2048;
@@ -373,8 +375,8 @@ extern "C" hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* 
     return hipGetLastError();
   }
   if (vx && vq) {
-    // With 64 floats per thread in registers, 4 workgroups per CU are resident (qz_cast
-    // holds 110 VGPRs); 1024 workgroups cover 4096 x 4096 in one chunk each.
+    // Up to 4 workgroups of 8 waves per CU (qz_amax holds 42 VGPRs, qz_cast 72, which
+    // leaves room for 3); 1024 workgroups cover 4096 x 4096 in one chunk each.
     const int g = grid_for(n, kChunk, 4);
     hipLaunchKernelGGL(qz_amax, dim3(g), dim3(kThreads), 0, stream, x, n, partial);
     e = hipGetLastError();
@@ -382,11 +384,12 @@ extern "C" hipError_t taskops_quantize_e4m3(const float* x, int64_t n, uint8_t* 
     hipLaunchKernelGGL(qz_cast, dim3(g), dim3(kThreads), 0, stream, x, n, partial, g, q, scale);
     return hipGetLastError();
   }
-  const int g1 = grid_for(n, (int64_t)kThreads * kPerThread, 4);
+  // 2 and 4 workgroups of 8 waves per CU: 16 and 32 waves.
+  const int g1 = grid_for(n, (int64_t)kThreads * kPerThread, 2);
   hipLaunchKernelGGL(qz_amax_any, dim3(g1), dim3(kThreads), 0, stream, x, n, partial);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int g2 = grid_for(n, (int64_t)kThreads * kPerThread, 8);
+  const int g2 = grid_for(n, (int64_t)kThreads * kPerThread, 4);
   hipLaunchKernelGGL(qz_cast_any, dim3(g2), dim3(kThreads), 0, stream, x, n, partial, g1, q, scale);
   return hipGetLastError();
 }

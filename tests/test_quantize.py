@@ -85,9 +85,11 @@ def _run_gpu(lib, x: torch.Tensor, q_off: int = 0, x_off: int = 0):
 
 
 # One workgroup of the fused path holds 16384 elements; tensors above its resident capacity
-# (about 20M elements) and unaligned ones take the two-pass path.
+# (1024 workgroups on 256 CUs, 2^24 elements) and unaligned ones take the two-pass path.
 @pytest.mark.gpu
-@pytest.mark.parametrize("n", [1, 15, 16, 17, 4095, 16384, 16385, 49151, 65537, 1 << 20, 24_000_001])
+@pytest.mark.parametrize(
+    "n", [1, 15, 16, 17, 4095, 16384, 16385, 49151, 65537, 1 << 20, 1 << 24, (1 << 24) + 1, 24_000_001]
+)
 def test_gpu_quantize_sizes(lib, n):
     print(f"\n[parity] quantize_e4m3 n={n}", flush=True)
     x = torch.randn(n, generator=torch.Generator().manual_seed(n)) * 3.0
