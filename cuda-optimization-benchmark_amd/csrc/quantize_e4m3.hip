@@ -233,6 +233,7 @@ constexpr int kQzLine = 16;  // unsigned per 64-byte line
 enum QzWord : int { kQzGroupCount = 0, kQzGroupMax = kQzGroups, kQzTopCount = 2 * kQzGroups, kQzSetWords };
 constexpr int kQzParity = 2 * kQzSetWords;  // after both sets
 constexpr int kQzWords = kQzParity + 1;
+static_assert(kQzSetWords <= kWave, "the grid's last arrival clears a set with one store per lane of a wave");
 constexpr unsigned kQzSpinDefault = 1u << 14;  // polls of the parity (~0.5-1 us each) before the fallback
 
 __device__ __forceinline__ unsigned* qz_word(unsigned* bar, unsigned set, int w, int i = 0) {
