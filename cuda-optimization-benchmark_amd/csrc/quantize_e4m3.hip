@@ -255,8 +255,9 @@ __device__ __forceinline__ unsigned qz_add(unsigned* p) {
 
 // Requires x 16-byte and q 4-byte aligned and gridDim.x = ceil(n / kChunk).  Thread 0 of
 // each workgroup runs the barrier; every RMW's returned value is used before the next
-// one is issued, which orders them at the coherence point.
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(5))) void qz_fused(
+// one is issued, which orders them at the coherence point.  8 waves per SIMD (at most 64
+// VGPRs) make 4 workgroups per CU resident, 1024 on 256 CUs: a 4096 x 4096 operand's chunks.
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(8))) void qz_fused(
     const float* __restrict__ x, int64_t n, uint8_t* __restrict__ q, float* __restrict__ scale_out,
     unsigned* __restrict__ bar, unsigned spin_limit) {
   __shared__ unsigned lds[kThreads / kWave];
