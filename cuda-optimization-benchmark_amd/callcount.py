@@ -145,6 +145,8 @@ def workloads():
         out.append((f"efficient_kan/{case['name']}", "efficient_kan", "efficient_kan_rowwise",
                     drop_in("efficient_kan", case)))
     out.append(("quantize_e4m3/aligned_n1000003", "quantize_e4m3", "quantize_e4m3_fused", quant(1_000_003, 0)))
+    # 4096 x 4096, the fused path's whole resident capacity: still one launch.
+    out.append(("quantize_e4m3/aligned_n16777216", "quantize_e4m3", "quantize_e4m3_fused", quant(1 << 24, 0)))
     out.append(("quantize_e4m3/aligned_n67108864", "quantize_e4m3", "quantize_e4m3", quant(1 << 26, 0)))
     out.append(("quantize_e4m3/unaligned_n4099", "quantize_e4m3", "quantize_e4m3", quant(4099, 1)))
     return out
